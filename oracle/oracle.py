@@ -1,0 +1,122 @@
+"""ctypes binding of the CPU restatement (liborc_q35.so).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke() and
+by bench.py's cpu_baseline leg, always as the checker or the timed CPU
+baseline, never as a path that produces product results.  The C sources it
+binds (q35_oracle.c) restate src/attn_qwen.c gqa_body (:235-397) and
+lin_body (:434-764) with the projections removed.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liborc_q35.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_lib = None
+
+
+def build() -> str:
+    """Compile liborc_q35.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "liborc_q35.so"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        i = ctypes.c_int
+        L.orc_gqa_body.argtypes = [i, i, i, i, _f32p, i, _f32p, _f32p, _f32p, _u16p, _u16p, _f32p]
+        L.orc_gqa_body.restype = i
+        L.orc_lin_body.argtypes = [i, i, i, i, i, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                   _u16p, _f32p, _u16p, _u16p, _f32p]
+        L.orc_lin_body.restype = i
+        L.orc_gqa_prefill.argtypes = [i, i, i, i, _f32p, i, i, _f32p, _f32p, _f32p, _u16p, _u16p,
+                                      _f32p]
+        L.orc_gqa_prefill.restype = i
+        L.orc_lin_prefill.argtypes = [i, i, i, i, i, i, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                      _u16p, _f32p, _u16p, _u16p, _f32p]
+        L.orc_lin_prefill.restype = i
+        L.orc_rope_table.argtypes = [i, i, ctypes.c_double, _f32p, _f32p]
+        L.orc_rope_table.restype = None
+        L.orc_rmsnorm.argtypes = [_u16p, i, _f32p]
+        L.orc_rmsnorm.restype = None
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def gqa_body(kv_layer, token, q, k, v, qn_w, kn_w, heads, kv_heads, head_dim):
+    """One decode token.  kv_layer [max_tokens][2*kv_heads*head_dim] fp32 is
+    updated in place; returns (attn_out [heads*head_dim], k after norm+RoPE)."""
+    assert kv_layer.dtype == np.float32 and kv_layer.flags["C_CONTIGUOUS"]
+    k = _c(k, np.float32).reshape(-1).copy()
+    out = np.zeros(heads * head_dim, np.float32)
+    rc = lib().orc_gqa_body(heads, kv_heads, head_dim, kv_layer.shape[0], kv_layer, token,
+                            _c(q, np.float32), k, _c(v, np.float32), _c(qn_w, np.uint16),
+                            _c(kn_w, np.uint16), out)
+    if rc != 0:
+        raise RuntimeError("orc_gqa_body failed")
+    return out, k
+
+
+def gqa_prefill(kv_layer, t0, q, k, v, qn_w, kn_w, heads, kv_heads, head_dim):
+    B = q.shape[0]
+    k = _c(k, np.float32).reshape(B, -1).copy()
+    out = np.zeros((B, heads * head_dim), np.float32)
+    rc = lib().orc_gqa_prefill(heads, kv_heads, head_dim, kv_layer.shape[0], kv_layer, t0, B,
+                               _c(q, np.float32), k, _c(v, np.float32), _c(qn_w, np.uint16),
+                               _c(kn_w, np.uint16), out)
+    if rc != 0:
+        raise RuntimeError("orc_gqa_prefill failed")
+    return out, k
+
+
+def lin_body(conv_ring, S, token, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w,
+             k_heads, v_heads, kd, vd):
+    """One decode token.  conv_ring [4][rows] and S [v_heads][kd][vd] are
+    updated in place; returns (out [v_heads*vd], qkv after conv + norm)."""
+    assert conv_ring.dtype == np.float32 and conv_ring.flags["C_CONTIGUOUS"]
+    assert S.dtype == np.float32 and S.flags["C_CONTIGUOUS"]
+    qkv = _c(qkv, np.float32).reshape(-1).copy()
+    out = np.zeros(v_heads * vd, np.float32)
+    rc = lib().orc_lin_body(k_heads, v_heads, kd, vd, token, conv_ring, S, qkv,
+                            _c(z, np.float32), _c(a, np.float32), _c(b, np.float32),
+                            _c(conv_w, np.uint16), _c(A_log, np.float32), _c(dt_bias, np.uint16),
+                            _c(norm_w, np.uint16), out)
+    if rc != 0:
+        raise RuntimeError("orc_lin_body failed")
+    return out, qkv
+
+
+def lin_prefill(conv_ring, S, t0, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w,
+                k_heads, v_heads, kd, vd):
+    B = qkv.shape[0]
+    qkv = _c(qkv, np.float32).copy()
+    out = np.zeros((B, v_heads * vd), np.float32)
+    rc = lib().orc_lin_prefill(k_heads, v_heads, kd, vd, t0, B, conv_ring, S, qkv,
+                               _c(z, np.float32), _c(a, np.float32), _c(b, np.float32),
+                               _c(conv_w, np.uint16), _c(A_log, np.float32),
+                               _c(dt_bias, np.uint16), _c(norm_w, np.uint16), out)
+    if rc != 0:
+        raise RuntimeError("orc_lin_prefill failed")
+    return out, qkv
+
+
+def rope_table(token, rd=64, theta=1e7):
+    c = np.zeros(rd // 2, np.float32)
+    s = np.zeros(rd // 2, np.float32)
+    lib().orc_rope_table(token, rd, theta, c, s)
+    return c, s

@@ -1,0 +1,89 @@
+/*
+ * q35_oracle.h -- CPU restatement of the Qwen3.5 hybrid-attention cores.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP path is compared
+ * against and the CPU baseline the benchmark times beside it; no product
+ * code links it.  It restates, in plain C99, the semantics of
+ *   src/attn_qwen.c  gqa_body          :235-397  (full-GQA core)
+ *   src/attn_qwen.c  lin_body          :434-764  (gated delta-rule core,
+ *                                                  scalar branch :657-717)
+ *   src/attn_qwen.c  ds4f_attn_gqa_chunk    :1222-1231 (serial prefill body loop)
+ *   src/attn_qwen.c  ds4f_attn_linear_chunk :1088-1109 (serial prefill body loop)
+ * with the projections (MLX-4bit matvecs) removed: the callers hand in the
+ * post-projection activations, exactly what the reference's bodies receive.
+ * It is compiled with gcc -std=c99 -O2 (no -mfma), which on x86-64 gives the
+ * same unfused float evaluation the reference's ISO-C scalar build has.
+ */
+#ifndef Q35_ORACLE_H
+#define Q35_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* bf16 bits -> float (src/attn_qwen.c:42-47). */
+float orc_bf16_f(uint16_t h);
+
+/* In-place RMSNorm, double sum of squares, eps 1e-6 on the mean, x/r*w
+ * (src/attn_qwen.c:50-55). */
+void orc_rmsnorm(const uint16_t *w, int dim, float *x);
+
+/* RoPE cos/sin of one position: rd/2 entries each, computed in double and
+ * cast (src/attn_qwen.c:297-307; theta fixed at 1e7 there). */
+void orc_rope_table(int token, int rd, double theta, float *cos_t, float *sin_t);
+
+/* Full-GQA body for one token (src/attn_qwen.c:235-397).
+ *   kv_layer : this layer's fp32 cache, [max_tokens][2*kv_heads*kh]
+ *              (k rows first, then v rows; src/attn_qwen.c:329-331)
+ *   q        : [heads][2*kh]  (q | gate per head), read only
+ *   k        : [kv_heads][kh] normed + rotated IN PLACE (as the reference)
+ *   v        : [kv_heads][kh]
+ *   attn_out : [heads][kh]
+ * Returns 0, or -1 on a geometry error.  token outside [0, max_tokens) is a
+ * silent skip (returns 0 and writes nothing), as src/attn_qwen.c:256. */
+int orc_gqa_body(int heads, int kv_heads, int kh, int max_tokens,
+                 float *kv_layer, int token, const float *q, float *k,
+                 const float *v, const uint16_t *qn_w, const uint16_t *kn_w,
+                 float *attn_out);
+
+/* Gated delta-rule body for one token, projections excluded
+ * (src/attn_qwen.c:470-764, scalar branch).
+ *   conv_ring : this layer's ring [4][qkv_rows], slot = token % 4
+ *   S         : this layer's state [v_heads][kd][vd] (row i = key dim)
+ *   qkv       : [qkv_rows] raw projection in; post-conv, normed values out
+ *               (the reference mutates it in place: :503, :535)
+ *   z         : [v_heads*vd]; a, b: [v_heads] (the in_proj_a / in_proj_b
+ *               outputs the reference computes at :462-468)
+ *   out       : [v_heads*vd] gated, normed readout (the o_proj input)
+ * qkv_rows = 2*k_heads*kd + v_heads*vd; value head h uses key head h/2
+ * (src/attn_qwen.c:658), so v_heads must equal 2*k_heads. */
+int orc_lin_body(int k_heads, int v_heads, int kd, int vd, int token,
+                 float *conv_ring, float *S, float *qkv, const float *z,
+                 const float *a, const float *b, const uint16_t *conv_w,
+                 const float *A_log, const uint16_t *dt_bias,
+                 const uint16_t *norm_w, float *out);
+
+/* Serial prefill: orc_gqa_body for t = t0 .. t0+B-1 in order
+ * (src/attn_qwen.c:1222-1231).  q: [B][heads*2*kh], k (in place), v:
+ * [B][kv_heads*kh], attn_out: [B][heads*kh]. */
+int orc_gqa_prefill(int heads, int kv_heads, int kh, int max_tokens,
+                    float *kv_layer, int t0, int B, const float *q, float *k,
+                    const float *v, const uint16_t *qn_w,
+                    const uint16_t *kn_w, float *attn_out);
+
+/* Serial prefill: orc_lin_body for t = t0 .. t0+B-1 in order
+ * (src/attn_qwen.c:1088-1109).  qkv: [B][qkv_rows] (in place), z/out:
+ * [B][v_heads*vd], a/b: [B][v_heads]. */
+int orc_lin_prefill(int k_heads, int v_heads, int kd, int vd, int t0, int B,
+                    float *conv_ring, float *S, float *qkv, const float *z,
+                    const float *a, const float *b, const uint16_t *conv_w,
+                    const float *A_log, const uint16_t *dt_bias,
+                    const uint16_t *norm_w, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q35_ORACLE_H */
