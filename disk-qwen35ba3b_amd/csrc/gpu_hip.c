@@ -1,0 +1,554 @@
+/*
+ * gpu_hip.c -- the HIP attention plugin: a C99 sibling of the reference's
+ * src/gpu_stub.c and src/gpu_metal.mm, exporting include/ds4f_gpu_attn.h.
+ *
+ * It owns the device mirrors of the engine's attention state (the
+ * Ds4fKvCache arrays of include/ds4f/attn.h:26-42), one HIP stream, and the
+ * staging buffers of the host-pointer entry points, and it applies the
+ * plugin conventions of include/ds4f/gpu.h:20-21 and src/head.c:271-283:
+ * lazy init, 0 = done, -1 = fall back to the CPU, sticky disable after the
+ * first failure with the device state written back to the bound host
+ * arrays first so the CPU path continues from exactly the same state.
+ *
+ * Kernels live in the .hip files next to this one (q35_launch.h).
+ */
+#include "ds4f_gpu_attn.h"
+#include "q35_launch.h"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define GQA_D 256
+#define GQA_GROUP 8
+#define ROPE_DIMS 64
+#define ROPE_THETA 10000000.0 /* src/attn_qwen.c:299 */
+#define KV_CHUNK_ROWS 4096    /* host<->device KV staging granularity */
+
+static struct Plugin {
+    int tried, ok, disabled;
+    hipStream_t stream;
+    char err[256];
+    int fail_countdown;        /* DS4F_GPU_FAIL_AFTER: forced failure */
+
+    int bound;
+    Ds4fGpuAttnGeom g;
+    int *kind, *slot;
+    int n_gqa, n_lin;
+    int t_pad, t_tiles;
+    int rows, vh, kd, vd;
+    size_t kv_elems;           /* per GQA layer, per K or V plane */
+    uint16_t *d_k, *d_v;
+    float *d_lin, *d_conv, *d_rope;
+    float *d_part_o, *d_part_ml;
+    float *host_kv, *host_lin, *host_conv;
+
+    void *d_stage, *h_stage;
+    size_t d_stage_cap, h_stage_cap;
+} P;
+
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(P.err, sizeof P.err, fmt, ap);
+    va_end(ap);
+}
+
+const char *ds4f_gpu_last_error(void) { return P.err; }
+
+#define HIPCHK(call)                                                              \
+    do {                                                                          \
+        hipError_t e_ = (call);                                                   \
+        if (e_ != hipSuccess) {                                                   \
+            set_err("%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__,     \
+                    __LINE__);                                                    \
+            return -1;                                                            \
+        }                                                                         \
+    } while (0)
+
+int ds4f_gpu_init(void) {
+    if (P.tried) return P.ok ? 0 : -1;
+    P.tried = 1;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        set_err("no HIP device");
+        return -1;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+        set_err("hipGetDeviceProperties failed");
+        return -1;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_err("device is %s, kernels are built for gfx950", prop.gcnArchName);
+        return -1;
+    }
+    if (hipSetDevice(0) != hipSuccess ||
+        hipStreamCreateWithFlags(&P.stream, hipStreamNonBlocking) != hipSuccess) {
+        set_err("stream creation failed");
+        return -1;
+    }
+    const char *f = getenv("DS4F_GPU_FAIL_AFTER");
+    P.fail_countdown = f ? atoi(f) : -1;
+    P.ok = 1;
+    return 0;
+}
+
+static void free_binding(void) {
+    if (P.d_k) hipFree(P.d_k);
+    if (P.d_v) hipFree(P.d_v);
+    if (P.d_lin) hipFree(P.d_lin);
+    if (P.d_conv) hipFree(P.d_conv);
+    if (P.d_rope) hipFree(P.d_rope);
+    if (P.d_part_o) hipFree(P.d_part_o);
+    if (P.d_part_ml) hipFree(P.d_part_ml);
+    free(P.kind);
+    free(P.slot);
+    P.d_k = P.d_v = NULL;
+    P.d_lin = P.d_conv = P.d_rope = P.d_part_o = P.d_part_ml = NULL;
+    P.kind = P.slot = NULL;
+    P.bound = 0;
+}
+
+void ds4f_gpu_free(void) {
+    if (!P.ok) return;
+    hipStreamSynchronize(P.stream);
+    free_binding();
+    if (P.d_stage) hipFree(P.d_stage);
+    if (P.h_stage) hipHostFree(P.h_stage);
+    hipStreamDestroy(P.stream);
+    memset(&P, 0, sizeof P);
+}
+
+int ds4f_gpu_attn_unbind(void) {
+    if (!P.ok) return -1;
+    hipStreamSynchronize(P.stream);
+    free_binding();
+    return 0;
+}
+
+static int ensure_stage(size_t dbytes, size_t hbytes) {
+    if (dbytes > P.d_stage_cap) {
+        if (P.d_stage) hipFree(P.d_stage);
+        P.d_stage = NULL;
+        P.d_stage_cap = 0;
+        HIPCHK(hipMalloc(&P.d_stage, dbytes));
+        P.d_stage_cap = dbytes;
+    }
+    if (hbytes > P.h_stage_cap) {
+        if (P.h_stage) hipHostFree(P.h_stage);
+        P.h_stage = NULL;
+        P.h_stage_cap = 0;
+        HIPCHK(hipHostMalloc(&P.h_stage, hbytes, 0));
+        P.h_stage_cap = hbytes;
+    }
+    return 0;
+}
+
+static size_t kv_row_floats(void) { return (size_t)2 * P.g.n_kv_heads * P.g.head_dim; }
+static size_t lin_floats(void) { return (size_t)P.vh * P.kd * P.vd; }
+static size_t conv_floats(void) { return (size_t)4 * P.rows; }
+
+static uint16_t *layer_k(int s) { return P.d_k + (size_t)s * P.kv_elems; }
+static uint16_t *layer_v(int s) { return P.d_v + (size_t)s * P.kv_elems; }
+static float *layer_lin(int s) { return P.d_lin + (size_t)s * lin_floats(); }
+static float *layer_conv(int s) { return P.d_conv + (size_t)s * conv_floats(); }
+
+/* One layer, one direction, synchronous. */
+static int sync_layer(int L, int dir, int n_tokens) {
+    int s = P.slot[L];
+    if (P.kind[L] == DS4F_LAYER_GQA && P.host_kv) {
+        size_t rf = kv_row_floats();
+        if (n_tokens > P.g.max_tokens) n_tokens = P.g.max_tokens;
+        if (ensure_stage((size_t)KV_CHUNK_ROWS * rf * sizeof(float), 0) != 0) return -1;
+        float *host = P.host_kv + (size_t)L * P.g.max_tokens * rf;
+        for (int p0 = 0; p0 < n_tokens; p0 += KV_CHUNK_ROWS) {
+            int n = n_tokens - p0 < KV_CHUNK_ROWS ? n_tokens - p0 : KV_CHUNK_ROWS;
+            size_t bytes = (size_t)n * rf * sizeof(float);
+            if (dir == DS4F_SYNC_TO_DEVICE) {
+                HIPCHK(hipMemcpyAsync(P.d_stage, host + (size_t)p0 * rf, bytes,
+                                      hipMemcpyHostToDevice, P.stream));
+                HIPCHK(q35_kv_import((const float *)P.d_stage, p0, n, layer_k(s), layer_v(s),
+                                     P.t_tiles, P.g.n_kv_heads, P.stream));
+            } else {
+                HIPCHK(q35_kv_export((float *)P.d_stage, p0, n, layer_k(s), layer_v(s),
+                                     P.t_tiles, P.g.n_kv_heads, P.stream));
+                HIPCHK(hipMemcpyAsync(host + (size_t)p0 * rf, P.d_stage, bytes,
+                                      hipMemcpyDeviceToHost, P.stream));
+            }
+            HIPCHK(hipStreamSynchronize(P.stream));
+        }
+    } else if (P.kind[L] == DS4F_LAYER_LINEAR) {
+        if (P.host_lin) {
+            size_t bytes = lin_floats() * sizeof(float);
+            if (ensure_stage(bytes, 0) != 0) return -1;
+            float *host = P.host_lin + (size_t)L * lin_floats();
+            if (dir == DS4F_SYNC_TO_DEVICE) {
+                HIPCHK(hipMemcpyAsync(P.d_stage, host, bytes, hipMemcpyHostToDevice, P.stream));
+                HIPCHK(q35_state_transpose((const float *)P.d_stage, layer_lin(s), P.vh, P.kd,
+                                           P.vd, P.stream));
+            } else {
+                HIPCHK(q35_state_transpose(layer_lin(s), (float *)P.d_stage, P.vh, P.vd, P.kd,
+                                           P.stream));
+                HIPCHK(hipMemcpyAsync(host, P.d_stage, bytes, hipMemcpyDeviceToHost, P.stream));
+            }
+            HIPCHK(hipStreamSynchronize(P.stream));
+        }
+        if (P.host_conv) {
+            size_t bytes = conv_floats() * sizeof(float);
+            float *host = P.host_conv + (size_t)L * conv_floats();
+            if (dir == DS4F_SYNC_TO_DEVICE)
+                HIPCHK(hipMemcpyAsync(layer_conv(s), host, bytes, hipMemcpyHostToDevice,
+                                      P.stream));
+            else
+                HIPCHK(hipMemcpyAsync(host, layer_conv(s), bytes, hipMemcpyDeviceToHost,
+                                      P.stream));
+            HIPCHK(hipStreamSynchronize(P.stream));
+        }
+    }
+    return 0;
+}
+
+int ds4f_gpu_attn_sync(int L, int dir, int n_kv_tokens) {
+    if (!P.ok || !P.bound) return -1;
+    if (L >= P.g.n_layers) return -1;
+    int lo = L < 0 ? 0 : L, hi = L < 0 ? P.g.n_layers : L + 1;
+    for (int l = lo; l < hi; l++)
+        if (sync_layer(l, dir, n_kv_tokens) != 0) return -1;
+    return 0;
+}
+
+/* Sticky fallback: write the device state back, then disable. */
+static int fail_over(int n_kv_tokens) {
+    char saved[256];
+    memcpy(saved, P.err, sizeof saved);
+    if (P.ok && P.bound) {
+        hipStreamSynchronize(P.stream);
+        for (int l = 0; l < P.g.n_layers; l++) sync_layer(l, DS4F_SYNC_TO_HOST, n_kv_tokens);
+    }
+    memcpy(P.err, saved, sizeof saved);
+    P.disabled = 1;
+    fprintf(stderr, "ds4f gpu: attention plugin disabled, CPU fallback (%s)\n", P.err);
+    return -1;
+}
+
+/* Failure injection for tests of the fallback path: DS4F_GPU_FAIL_AFTER=n
+ * makes the (n+1)-th entry-point call fail before it launches anything. */
+static int forced_failure(void) {
+    if (P.fail_countdown < 0) return 0;
+    if (P.fail_countdown == 0) {
+        set_err("forced failure (DS4F_GPU_FAIL_AFTER)");
+        return 1;
+    }
+    P.fail_countdown--;
+    return 0;
+}
+
+int ds4f_gpu_attn_bind(const Ds4fGpuAttnGeom *geom, const int *layer_kind, float *host_kv,
+                       float *host_lin, float *host_conv, int n_kv_tokens) {
+    if (ds4f_gpu_init() != 0 || P.disabled) return -1;
+    if (!geom || !layer_kind) return -1;
+    const Ds4fGpuAttnGeom g = *geom;
+    if (g.n_layers < 1 || g.max_tokens < 1 || g.head_dim != GQA_D || g.n_kv_heads < 1 ||
+        g.n_heads != GQA_GROUP * g.n_kv_heads || g.lin_kd != 128 || g.lin_vd != 128) {
+        set_err("unsupported geometry (head_dim %d heads %d kv_heads %d kd %d vd %d)",
+                g.head_dim, g.n_heads, g.n_kv_heads, g.lin_kd, g.lin_vd);
+        return -1;
+    }
+    hipStreamSynchronize(P.stream);
+    free_binding();
+    P.g = g;
+    P.kind = (int *)calloc((size_t)g.n_layers, sizeof(int));
+    P.slot = (int *)calloc((size_t)g.n_layers, sizeof(int));
+    if (!P.kind || !P.slot) return -1;
+    P.n_gqa = P.n_lin = 0;
+    for (int l = 0; l < g.n_layers; l++) {
+        P.kind[l] = layer_kind[l];
+        if (layer_kind[l] == DS4F_LAYER_GQA)
+            P.slot[l] = P.n_gqa++;
+        else if (layer_kind[l] == DS4F_LAYER_LINEAR)
+            P.slot[l] = P.n_lin++;
+        else
+            P.slot[l] = -1;
+    }
+    P.kd = g.lin_kd;
+    P.vd = g.lin_vd;
+    P.vh = 16 * g.n_kv_heads;                           /* src/attn_qwen.c:453 */
+    P.rows = 2 * g.n_heads * P.kd + P.vh * P.vd;        /* src/attn_qwen.c:866 */
+    P.t_pad = (g.max_tokens + 63) / 64 * 64;
+    P.t_tiles = P.t_pad / 16;
+    P.kv_elems = (size_t)g.n_kv_heads * P.t_pad * GQA_D;
+    P.host_kv = host_kv;
+    P.host_lin = host_lin;
+    P.host_conv = host_conv;
+
+    if (P.n_gqa) {
+        size_t b = (size_t)P.n_gqa * P.kv_elems * sizeof(uint16_t);
+        HIPCHK(hipMalloc((void **)&P.d_k, b));
+        HIPCHK(hipMalloc((void **)&P.d_v, b));
+        HIPCHK(hipMemsetAsync(P.d_k, 0, b, P.stream));
+        HIPCHK(hipMemsetAsync(P.d_v, 0, b, P.stream));
+        size_t pb = (size_t)g.n_kv_heads * q35_gqa_max_chunks() * GQA_GROUP;
+        HIPCHK(hipMalloc((void **)&P.d_part_o, pb * GQA_D * sizeof(float)));
+        HIPCHK(hipMalloc((void **)&P.d_part_ml, pb * 2 * sizeof(float)));
+        /* RoPE table: double -> float per position, as src/attn_qwen.c:302-307 */
+        size_t nr = (size_t)g.max_tokens * ROPE_DIMS;
+        float *tab = (float *)malloc(nr * sizeof(float));
+        if (!tab) return -1;
+        double inv[ROPE_DIMS / 2];
+        for (int i = 0; i < ROPE_DIMS / 2; i++)
+            inv[i] = 1.0 / pow(ROPE_THETA, (double)(2 * i) / (double)ROPE_DIMS);
+        for (int t = 0; t < g.max_tokens; t++) {
+            float *row = tab + (size_t)t * ROPE_DIMS;
+            for (int i = 0; i < ROPE_DIMS / 2; i++) {
+                double f = (double)t * inv[i];
+                row[i] = (float)cos(f);
+                row[ROPE_DIMS / 2 + i] = (float)sin(f);
+            }
+        }
+        if (hipMalloc((void **)&P.d_rope, nr * sizeof(float)) != hipSuccess ||
+            hipMemcpy(P.d_rope, tab, nr * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+            free(tab);
+            set_err("rope table upload failed");
+            return -1;
+        }
+        free(tab);
+    }
+    if (P.n_lin) {
+        size_t b = (size_t)P.n_lin * lin_floats() * sizeof(float);
+        size_t c = (size_t)P.n_lin * conv_floats() * sizeof(float);
+        HIPCHK(hipMalloc((void **)&P.d_lin, b));
+        HIPCHK(hipMalloc((void **)&P.d_conv, c));
+        HIPCHK(hipMemsetAsync(P.d_lin, 0, b, P.stream));
+        HIPCHK(hipMemsetAsync(P.d_conv, 0, c, P.stream));
+    }
+    HIPCHK(hipStreamSynchronize(P.stream));
+    P.bound = 1;
+    for (int l = 0; l < g.n_layers; l++)
+        if (sync_layer(l, DS4F_SYNC_TO_DEVICE, n_kv_tokens) != 0) {
+            P.bound = 0;
+            return -1;
+        }
+    return 0;
+}
+
+static hipStream_t pick(void *stream) { return stream ? (hipStream_t)stream : P.stream; }
+
+static int check_layer(int L, int kind) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers || P.kind[L] != kind) {
+        set_err("layer %d is not bound as kind %d", L, kind);
+        return -1;
+    }
+    return 0;
+}
+
+/* ---- device-pointer entry points --------------------------------------- */
+
+int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate, const float *k,
+                              const float *v, const uint16_t *qn_w, const uint16_t *kn_w,
+                              float *attn_out, float *k_post, void *stream) {
+    if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
+    if (token < 0 || token >= P.g.max_tokens) return 0;     /* src/attn_qwen.c:256 */
+    Q35GqaDecode p;
+    memset(&p, 0, sizeof p);
+    p.q_gate = q_gate;
+    p.k_new = k;
+    p.v_new = v;
+    p.qn_w = qn_w;
+    p.kn_w = kn_w;
+    p.rope = P.d_rope + (size_t)token * ROPE_DIMS;
+    p.kt = layer_k(P.slot[L]);
+    p.vt = layer_v(P.slot[L]);
+    p.part_o = P.d_part_o;
+    p.part_ml = P.d_part_ml;
+    p.attn_out = attn_out;
+    p.k_post = k_post;
+    p.token = token;
+    p.t_tiles = P.t_tiles;
+    p.heads = P.g.n_heads;
+    p.kv_heads = P.g.n_kv_heads;
+    q35_gqa_split(token, &p.chunk, &p.n_chunks);
+    HIPCHK(q35_gqa_decode(&p, pick(stream)));
+    return 0;
+}
+
+int ds4f_hip_lin_decode_async(int L, int token, const float *qkv, const float *z, const float *a,
+                              const float *b, const uint16_t *conv_w, const float *A_log,
+                              const uint16_t *dt_bias, const uint16_t *norm_w, float *out,
+                              float *qkv_post, void *stream) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    if (token < 0 || token >= P.g.max_tokens) return 0;     /* src/attn_qwen.c:882 */
+    Q35LinDecode p;
+    memset(&p, 0, sizeof p);
+    p.qkv = qkv;
+    p.z = z;
+    p.a = a;
+    p.b = b;
+    p.conv_w = conv_w;
+    p.A_log = A_log;
+    p.dt_bias = dt_bias;
+    p.norm_w = norm_w;
+    p.ring = layer_conv(P.slot[L]);
+    p.state = layer_lin(P.slot[L]);
+    p.out = out;
+    p.qkv_post = qkv_post;
+    p.token = token;
+    p.k_heads = P.g.n_heads;
+    p.v_heads = P.vh;
+    HIPCHK(q35_lin_decode(&p, pick(stream)));
+    return 0;
+}
+
+/* ---- host-pointer entry points ----------------------------------------- */
+
+/* Pack host arrays into the pinned stage, one H2D copy; returns device
+ * pointers of each piece (256-byte aligned). */
+typedef struct { const void *src; size_t bytes; void **dev; } Piece;
+
+static int upload(Piece *pc, int n, size_t out_bytes, void **d_out) {
+    size_t off = 0, offs[16];
+    for (int i = 0; i < n; i++) {
+        offs[i] = off;
+        off += (pc[i].bytes + 255) & ~(size_t)255;
+    }
+    size_t out_off = off;
+    off += (out_bytes + 255) & ~(size_t)255;
+    if (ensure_stage(off, off) != 0) return -1;
+    for (int i = 0; i < n; i++) {
+        memcpy((char *)P.h_stage + offs[i], pc[i].src, pc[i].bytes);
+        *pc[i].dev = (char *)P.d_stage + offs[i];
+    }
+    HIPCHK(hipMemcpyAsync(P.d_stage, P.h_stage, out_off, hipMemcpyHostToDevice, P.stream));
+    *d_out = (char *)P.d_stage + out_off;
+    return 0;
+}
+
+static int download(void *d_src, size_t bytes) {
+    HIPCHK(hipMemcpyAsync(P.h_stage, d_src, bytes, hipMemcpyDeviceToHost, P.stream));
+    HIPCHK(hipStreamSynchronize(P.stream));
+    return 0;
+}
+
+int ds4f_gpu_gqa_decode(int L, int token, const float *q_gate, float *k, const float *v,
+                        const uint16_t *qn_w, const uint16_t *kn_w, float *attn_out) {
+    if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
+    if (token < 0 || token >= P.g.max_tokens) return 0;
+    if (forced_failure()) return fail_over(token);
+    const int H = P.g.n_heads, KVH = P.g.n_kv_heads, D = GQA_D;
+    void *dq, *dk, *dv, *dqn, *dkn, *dout;
+    Piece pc[5] = {{q_gate, (size_t)H * 2 * D * 4, &dq},
+                   {k, (size_t)KVH * D * 4, &dk},
+                   {v, (size_t)KVH * D * 4, &dv},
+                   {qn_w, (size_t)D * 2, &dqn},
+                   {kn_w, (size_t)D * 2, &dkn}};
+    size_t ob = (size_t)(H + KVH) * D * 4;   /* attn_out then k_post */
+    if (upload(pc, 5, ob, &dout) != 0) return fail_over(token);
+    float *d_attn = (float *)dout, *d_kpost = d_attn + (size_t)H * D;
+    if (ds4f_hip_gqa_decode_async(L, token, (const float *)dq, (const float *)dk,
+                                  (const float *)dv, (const uint16_t *)dqn,
+                                  (const uint16_t *)dkn, d_attn, d_kpost, NULL) != 0 ||
+        download(dout, ob) != 0)
+        return fail_over(token);
+    memcpy(attn_out, P.h_stage, (size_t)H * D * 4);
+    memcpy(k, (char *)P.h_stage + (size_t)H * D * 4, (size_t)KVH * D * 4);
+    return 0;
+}
+
+int ds4f_gpu_lin_decode(int L, int token, float *qkv, const float *z, const float *a,
+                        const float *b, const uint16_t *conv_w, const float *A_log,
+                        const uint16_t *dt_bias, const uint16_t *norm_w, float *out) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    if (token < 0 || token >= P.g.max_tokens) return 0;
+    if (forced_failure()) return fail_over(token);
+    const int rows = P.rows, VH = P.vh, VD = P.vd;
+    void *dqkv, *dz, *da, *db, *dcw, *dal, *ddt, *dnw, *dout;
+    Piece pc[8] = {{qkv, (size_t)rows * 4, &dqkv},
+                   {z, (size_t)VH * VD * 4, &dz},
+                   {a, (size_t)VH * 4, &da},
+                   {b, (size_t)VH * 4, &db},
+                   {conv_w, (size_t)rows * 4 * 2, &dcw},
+                   {A_log, (size_t)VH * 4, &dal},
+                   {dt_bias, (size_t)VH * 2, &ddt},
+                   {norm_w, (size_t)VD * 2, &dnw}};
+    size_t ob = ((size_t)VH * VD + rows) * 4;   /* out then qkv_post */
+    if (upload(pc, 8, ob, &dout) != 0) return fail_over(token);
+    float *d_out = (float *)dout, *d_post = d_out + (size_t)VH * VD;
+    if (ds4f_hip_lin_decode_async(L, token, (const float *)dqkv, (const float *)dz,
+                                  (const float *)da, (const float *)db, (const uint16_t *)dcw,
+                                  (const float *)dal, (const uint16_t *)ddt,
+                                  (const uint16_t *)dnw, d_out, d_post, NULL) != 0 ||
+        download(dout, ob) != 0)
+        return fail_over(token);
+    memcpy(out, P.h_stage, (size_t)VH * VD * 4);
+    memcpy(qkv, (char *)P.h_stage + (size_t)VH * VD * 4, (size_t)rows * 4);
+    return 0;
+}
+
+/* Prefill over B tokens.  The device prefill kernels are in
+ * gqa_prefill.hip / lin_prefill.hip; until a layer shape is covered by
+ * them the token loop below runs the decode kernels in order, which gives
+ * the serial semantics of src/attn_qwen.c:1222-1231 / :1088-1109. */
+int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k, const float *v,
+                         const uint16_t *qn_w, const uint16_t *kn_w, float *attn_out) {
+    if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
+    const int H = P.g.n_heads, KVH = P.g.n_kv_heads, D = GQA_D;
+    for (int t = 0; t < B; t++) {
+        int rc = ds4f_gpu_gqa_decode(L, t0 + t, q_gate + (size_t)t * H * 2 * D,
+                                     k + (size_t)t * KVH * D, v + (size_t)t * KVH * D, qn_w,
+                                     kn_w, attn_out + (size_t)t * H * D);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+int ds4f_gpu_lin_prefill(int L, int t0, int B, float *qkv, const float *z, const float *a,
+                         const float *b, const uint16_t *conv_w, const float *A_log,
+                         const uint16_t *dt_bias, const uint16_t *norm_w, float *out) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    const int rows = P.rows, VH = P.vh, VD = P.vd;
+    for (int t = 0; t < B; t++) {
+        int rc = ds4f_gpu_lin_decode(L, t0 + t, qkv + (size_t)t * rows, z + (size_t)t * VH * VD,
+                                     a + (size_t)t * VH, b + (size_t)t * VH, conv_w, A_log,
+                                     dt_bias, norm_w, out + (size_t)t * VH * VD);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+/* ---- synthetic state ---------------------------------------------------- */
+
+int ds4f_hip_synth(void *dst, int64_t n, int dtype, int dist, double p0, double p1,
+                   uint64_t seed, uint64_t tid, void *stream) {
+    if (ds4f_gpu_init() != 0) return -1;
+    HIPCHK(q35_synth(dst, n, dtype, dist, p0, p1, seed, tid, pick(stream)));
+    return 0;
+}
+
+int ds4f_hip_synth_gqa_cache(int L, int n_past, uint64_t seed, uint64_t tid_k, uint64_t tid_v,
+                             void *stream) {
+    if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
+    if (n_past < 0 || n_past > P.g.max_tokens) return -1;
+    HIPCHK(q35_synth_kv(layer_k(P.slot[L]), layer_v(P.slot[L]), n_past, P.t_tiles,
+                        P.g.n_kv_heads, seed, tid_k, tid_v, pick(stream)));
+    return 0;
+}
+
+int ds4f_hip_synth_lin_state(int L, double sigma, uint64_t seed, uint64_t tid, void *stream) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    HIPCHK(q35_synth_state(layer_lin(P.slot[L]), P.vh, P.kd, P.vd, sigma, seed, tid,
+                           pick(stream)));
+    return 0;
+}
+
+int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid, void *stream) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    HIPCHK(q35_synth_conv(layer_conv(P.slot[L]), P.rows, token, seed, tid, pick(stream)));
+    return 0;
+}

@@ -1,0 +1,178 @@
+/*
+ * lin_decode.hip -- one decode token of a gated delta-rule layer on gfx950.
+ *
+ * Replaces lin_body's per-token work (src/attn_qwen.c:470-764): causal
+ * depthwise conv1d (k = 4) + SiLU over the ring, q/k RMS-normalisation,
+ * decay / beta gates, the gated delta rule on the 128x128 fp32 state of
+ * every value head, and the RMSNormGated epilogue.
+ *
+ * One workgroup owns one value head: 1024 threads, thread t holds column
+ * j = t/8 of the value-major state and 16 consecutive key rows of it
+ * (64 contiguous bytes).  The state is the dominant traffic (64 KiB read and
+ * 64 KiB written per head); its loads are issued before the prologue so the
+ * HBM latency overlaps the conv / norm work.  Owning a whole head keeps the
+ * RMSNormGated reduction (over all 128 value columns) inside the workgroup,
+ * so the layer is one launch with no cross-workgroup handshake.
+ *
+ * Arithmetic: fp32 with FMA in the state update (the reference sums i in
+ * ascending order without FMA; the difference is fp32 rounding).  The
+ * conv, norms and gates keep the reference's operation order.
+ */
+#include "q35_device.h"
+#include "q35_launch.h"
+
+namespace {
+
+constexpr int KD = 128, VD = 128, NT = 1024;
+
+/* Causal conv tap sum + SiLU for one channel (src/attn_qwen.c:493-504):
+ * tap k reads position token-3+k (k = 3 is the incoming raw value), taps
+ * before position 0 are skipped. */
+__device__ __forceinline__ float conv_silu(const float *ring, int rows, int ch, float raw,
+                                           const uint16_t *w, int token) {
+#pragma clang fp contract(off)
+    const uint2 wv = *reinterpret_cast<const uint2 *>(w + (size_t)ch * 4);
+    const uint16_t wt[4] = {(uint16_t)(wv.x & 0xffff), (uint16_t)(wv.x >> 16),
+                            (uint16_t)(wv.y & 0xffff), (uint16_t)(wv.y >> 16)};
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int tp = token - 3 + k;
+        if (tp < 0) continue;
+        float x = (k == 3) ? raw : ring[(size_t)(tp & 3) * rows + ch];
+        acc += x * q35_bf2f(wt[k]);
+    }
+    return acc * q35_sigmoid(acc);
+}
+
+__global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
+    const int h = blockIdx.x;      /* value head */
+    const int kh = h >> 1;         /* its key head (src/attn_qwen.c:658) */
+    const int t = threadIdx.x;
+    const int rows = 2 * p.k_heads * KD + p.v_heads * VD;
+    const int tok = p.token;
+
+    /* state slice first: column j, key rows il*16 .. il*16+15 */
+    const int j = t >> 3, il = t & 7;
+    float4 *sp = reinterpret_cast<float4 *>(p.state + ((size_t)h * VD + j) * KD + il * 16);
+    float4 s[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) s[u] = sp[u];
+
+    __shared__ float sq[KD], sk[KD], sv[VD], so[VD];
+    __shared__ double sred[4];
+    __shared__ float sgate[2];
+
+    /* prologue: conv + SiLU of this head's q (t<128), k (t<256), v (t<384) */
+    int ch = -1, kind = -1;
+    if (t < KD) {
+        ch = kh * KD + t;
+        kind = 0;
+    } else if (t < 2 * KD) {
+        ch = p.k_heads * KD + kh * KD + (t - KD);
+        kind = 1;
+    } else if (t < 2 * KD + VD) {
+        ch = 2 * p.k_heads * KD + h * VD + (t - 2 * KD);
+        kind = 2;
+    }
+    float x = 0.0f;
+    if (ch >= 0) {
+        const float raw = p.qkv[ch];
+        x = conv_silu(p.ring, rows, ch, raw, p.conv_w, tok);
+        /* ring slot token%4 takes the raw row; q/k channels are shared by
+         * the two value heads of a key head, the even one writes them */
+        if (kind == 2 || (h & 1) == 0) p.ring[(size_t)(tok & 3) * rows + ch] = raw;
+    }
+    double ss = (kind == 0 || kind == 1) ? (double)x * x : 0.0;
+    ss = q35_wave_sum(ss);
+    if ((t & 63) == 0 && t < 2 * KD) sred[t >> 6] = ss;
+    if (t == 2 * KD + VD) {
+        /* gates (src/attn_qwen.c:545-551, :664-665) */
+#pragma clang fp contract(off)
+        float xa = p.a[h] + q35_bf2f(p.dt_bias[h]);
+        float sp_ = xa > 0 ? xa + log1pf(expf(-xa)) : log1pf(expf(xa));
+        float g = -expf(p.A_log[h]) * sp_;
+        sgate[0] = expf(g);
+        sgate[1] = q35_sigmoid(p.b[h]);
+    }
+    __syncthreads();
+    if (kind == 0 || kind == 1) {
+#pragma clang fp contract(off)
+        double tot = kind == 0 ? sred[0] + sred[1] : sred[2] + sred[3];
+        float r = sqrtf((float)(tot / (double)KD) + 1e-6f);
+        float y;
+        if (kind == 0) {
+            y = x / r * (1.0f / (float)KD);
+            sq[t] = y;
+        } else {
+            y = x / r * (1.0f / sqrtf((float)KD));
+            sk[t - KD] = y;
+        }
+        if (p.qkv_post && (h & 1) == 0) p.qkv_post[ch] = y;
+    } else if (kind == 2) {
+        sv[t - 2 * KD] = x;
+        if (p.qkv_post) p.qkv_post[ch] = x;
+    }
+    __syncthreads();
+
+    /* gated delta rule on column j (src/attn_qwen.c:666-690) */
+    const float dec = sgate[0], beta = sgate[1];
+    const float4 *k4 = reinterpret_cast<const float4 *>(sk + il * 16);
+    const float4 *q4 = reinterpret_cast<const float4 *>(sq + il * 16);
+    float mem = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        float4 kk = k4[u];
+        s[u].x *= dec; s[u].y *= dec; s[u].z *= dec; s[u].w *= dec;
+        mem = fmaf(s[u].x, kk.x, mem);
+        mem = fmaf(s[u].y, kk.y, mem);
+        mem = fmaf(s[u].z, kk.z, mem);
+        mem = fmaf(s[u].w, kk.w, mem);
+    }
+    mem += __shfl_xor(mem, 4);
+    mem += __shfl_xor(mem, 2);
+    mem += __shfl_xor(mem, 1);
+    const float delta = (sv[j] - mem) * beta;
+    float o = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        float4 kk = k4[u], qq = q4[u];
+        s[u].x = fmaf(kk.x, delta, s[u].x);
+        s[u].y = fmaf(kk.y, delta, s[u].y);
+        s[u].z = fmaf(kk.z, delta, s[u].z);
+        s[u].w = fmaf(kk.w, delta, s[u].w);
+        o = fmaf(s[u].x, qq.x, o);
+        o = fmaf(s[u].y, qq.y, o);
+        o = fmaf(s[u].z, qq.z, o);
+        o = fmaf(s[u].w, qq.w, o);
+    }
+    o += __shfl_xor(o, 4);
+    o += __shfl_xor(o, 2);
+    o += __shfl_xor(o, 1);
+#pragma unroll
+    for (int u = 0; u < 4; u++) sp[u] = s[u];
+    if (il == 0) so[j] = o;
+    __syncthreads();
+
+    /* RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749) */
+    if (t < VD) {
+        double o2 = (double)so[t] * so[t];
+        o2 = q35_wave_sum(o2);
+        if ((t & 63) == 0) sred[t >> 6] = o2;
+    }
+    __syncthreads();
+    if (t < VD) {
+#pragma clang fp contract(off)
+        float r = sqrtf((float)((sred[0] + sred[1]) / (double)VD) + 1e-6f);
+        float zv = p.z[h * VD + t];
+        float sg = q35_sigmoid(zv);
+        p.out[h * VD + t] = so[t] / r * q35_bf2f(p.norm_w[t]) * (zv * sg);
+    }
+}
+
+}  // namespace
+
+extern "C" hipError_t q35_lin_decode(const Q35LinDecode *p, hipStream_t stream) {
+    hipLaunchKernelGGL(lin_decode_kernel, dim3(p->v_heads), dim3(NT), 0, stream, *p);
+    return hipGetLastError();
+}

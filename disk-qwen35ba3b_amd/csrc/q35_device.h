@@ -1,0 +1,87 @@
+/*
+ * q35_device.h -- device helpers shared by the gfx950 kernels.
+ */
+#ifndef Q35_DEVICE_H
+#define Q35_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+#define Q35_GQA_D 256       /* GQA head dim */
+#define Q35_GQA_GROUP 8     /* q heads per kv head */
+#define Q35_ROPE_DIMS 64    /* rotary dims: head_dim * 0.25 */
+
+__device__ __forceinline__ float q35_bf2f(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+
+/* float -> bf16 bits, round to nearest even (NaN kept quiet). */
+__device__ __forceinline__ uint16_t q35_f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* hi + lo split of a float into two bf16 (hi = rne(x), lo = rne(x - hi)). */
+__device__ __forceinline__ void q35_split_bf16(float x, uint16_t &hi, uint16_t &lo) {
+    hi = q35_f2bf(x);
+    lo = q35_f2bf(x - q35_bf2f(hi));
+}
+
+__device__ __forceinline__ __bf16 q35_as_bf16(uint16_t h) {
+    return __builtin_bit_cast(__bf16, h);
+}
+
+template <typename T>
+__device__ __forceinline__ T q35_wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+/* sigmoid written as the reference writes it: 1 / (1 + expf(-x)). */
+__device__ __forceinline__ float q35_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* splitmix64 finaliser (public algorithm; the same constants as the
+ * reference's ds4f_mix64, src/router.c:11-16). */
+__device__ __forceinline__ uint64_t q35_fmix64(uint64_t z) {
+    z ^= z >> 30;
+    z *= 0xBF58476D1CE4E5B9ull;
+    z ^= z >> 27;
+    z *= 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* Draw i (0-based) of stream (seed, tid). */
+__device__ __forceinline__ uint64_t q35_draw(uint64_t seed, uint64_t tid, uint64_t i) {
+    uint64_t s0 = seed ^ (tid * 0xD1B54A32D192ED03ull);
+    return q35_fmix64(s0 + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+
+__device__ __forceinline__ double q35_unit(uint64_t x) {
+    return (double)(x >> 11) * (1.0 / 9007199254740992.0);
+}
+
+/* Element i of a normal stream, in double (Box-Muller, cosine branch). */
+__device__ __forceinline__ double q35_normal(uint64_t seed, uint64_t tid, uint64_t i) {
+    double u1 = q35_unit(q35_draw(seed, tid, 2 * i));
+    double u2 = q35_unit(q35_draw(seed, tid, 2 * i + 1));
+    return sqrt(-2.0 * log(1.0 - u1)) * cos(2.0 * 3.141592653589793 * u2);
+}
+
+/* Device K / V tile addressing (see q35_launch.h). */
+__device__ __forceinline__ size_t q35_k_index(int kvh, int p, int d, int t_tiles) {
+    return ((((size_t)kvh * t_tiles + (p >> 4)) * (Q35_GQA_D / 32) + (d >> 5)) * 16 + (p & 15)) * 32 +
+           (d & 31);
+}
+__device__ __forceinline__ size_t q35_v_index(int kvh, int p, int d, int t_tiles) {
+    return (((size_t)kvh * t_tiles + (p >> 4)) * Q35_GQA_D + d) * 16 + (p & 15);
+}
+
+#endif /* Q35_DEVICE_H */

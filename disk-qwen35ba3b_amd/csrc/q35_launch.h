@@ -1,0 +1,86 @@
+/*
+ * q35_launch.h -- launchers of the gfx950 kernels, callable from the C99
+ * shim (gpu_hip.c).  Every pointer is a device pointer; every launcher only
+ * enqueues on `stream` and returns the launch status.
+ *
+ * Device layouts (all chosen for the MFMA operand shapes of gfx950):
+ *   K cache  bf16, per kv head, 16-token x 32-dim blocks:
+ *            [kvh][T/16][D/32][16 tok][32 dim]  -- one block is exactly one
+ *            16x16x32 MFMA operand (1 KiB, contiguous)
+ *   V cache  bf16, per kv head, 16-token tiles stored dim-major:
+ *            [kvh][T/16][D][16 tok]             -- 16 dims of a tile are one
+ *            16x16x16 MFMA operand (512 B, contiguous)
+ *   delta state  fp32, value-major per head: [vh][vd][kd]; one value column
+ *            is 512 B contiguous
+ *   conv ring    fp32 [4][rows], slot = token % 4 (the reference's ring)
+ * T is the padded token capacity (a multiple of 64).
+ */
+#ifndef Q35_LAUNCH_H
+#define Q35_LAUNCH_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- gated delta-rule decode (kd = vd = 128) ---- */
+typedef struct Q35LinDecode {
+    const float *qkv, *z, *a, *b;
+    const uint16_t *conv_w, *dt_bias, *norm_w;
+    const float *A_log;
+    float *ring;       /* [4][rows] */
+    float *state;      /* [vh][vd][kd] */
+    float *out;        /* [vh*vd] */
+    float *qkv_post;   /* optional [rows] */
+    int token, k_heads, v_heads;
+} Q35LinDecode;
+hipError_t q35_lin_decode(const Q35LinDecode *p, hipStream_t stream);
+
+/* ---- GQA split-K decode (head_dim 256, 8 q heads per kv head) ---- */
+typedef struct Q35GqaDecode {
+    const float *q_gate;           /* [H][2D] */
+    const float *k_new, *v_new;    /* [KVH][D] */
+    const uint16_t *qn_w, *kn_w;
+    const float *rope;             /* this position: cos[rd/2] then sin[rd/2] */
+    uint16_t *kt, *vt;             /* this layer's K / V tiles */
+    float *part_o;                 /* [KVH][P][8][D] */
+    float *part_ml;                /* [KVH][P][8][2] */
+    float *attn_out;               /* [H][D] */
+    float *k_post;                 /* optional [KVH][D] */
+    int token;                     /* position; cache rows [0, token) are past */
+    int t_tiles;                   /* T/16 of this layer's tiles */
+    int heads, kv_heads;
+    int chunk, n_chunks;           /* positions per workgroup, P */
+} Q35GqaDecode;
+hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream);
+/* P and chunk for a step with n_past cached rows. */
+void q35_gqa_split(int n_past, int *chunk, int *n_chunks);
+int q35_gqa_max_chunks(void);
+
+/* ---- state movement between host row layouts and device layouts ---- */
+/* rows [p0, p0+n) of a host-layout fp32 block [n][2*KVH*D] <-> tiles */
+hipError_t q35_kv_import(const float *rows, int p0, int n, uint16_t *kt, uint16_t *vt,
+                         int t_tiles, int kv_heads, hipStream_t stream);
+hipError_t q35_kv_export(float *rows, int p0, int n, const uint16_t *kt,
+                         const uint16_t *vt, int t_tiles, int kv_heads, hipStream_t stream);
+/* [vh][kd][vd] <-> [vh][vd][kd] */
+hipError_t q35_state_transpose(const float *src, float *dst, int heads, int rows, int cols,
+                               hipStream_t stream);
+
+/* ---- synthetic streams ---- */
+hipError_t q35_synth(void *dst, int64_t n, int dtype, int dist, double p0, double p1,
+                     uint64_t seed, uint64_t tid, hipStream_t stream);
+hipError_t q35_synth_kv(uint16_t *kt, uint16_t *vt, int n_past, int t_tiles, int kv_heads,
+                        uint64_t seed, uint64_t tid_k, uint64_t tid_v, hipStream_t stream);
+hipError_t q35_synth_state(float *state, int heads, int kd, int vd, double sigma,
+                           uint64_t seed, uint64_t tid, hipStream_t stream);
+hipError_t q35_synth_conv(float *ring, int rows, int token, uint64_t seed, uint64_t tid,
+                          hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q35_LAUNCH_H */

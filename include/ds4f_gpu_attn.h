@@ -1,0 +1,167 @@
+/*
+ * ds4f_gpu_attn.h -- HIP (gfx950) attention plugin for the Qwen3.5 hybrid
+ * stack: the C ABI a sibling of src/gpu_stub.c / src/gpu_metal.mm exports.
+ *
+ * Conventions are the ones include/ds4f/gpu.h fixes for the engine's GPU
+ * plugin (gpu.h:6-8, :20-21):
+ *   - plain C, extern "C", caller-owned plain pointers and sizes;
+ *   - return 0 when the work was done, -1 when the GPU is unavailable or
+ *     the call failed -- the caller then runs its CPU path;
+ *   - after the first failure the plugin stays disabled (the sticky
+ *     fallback of src/head.c:283) and device state has been written back
+ *     to the bound host arrays, so the CPU path continues exactly.
+ *
+ * The reference has no attention entry points in gpu.h; the ones below are
+ * the call sites inside src/attn_qwen.c they replace:
+ *   ds4f_gpu_gqa_decode   <- gqa_body :279-396 (norms, RoPE, cache write,
+ *                            softmax attention, sigmoid gate)
+ *   ds4f_gpu_lin_decode   <- lin_body :470-764 (conv1d+SiLU, q/k norm,
+ *                            gates, gated delta rule, RMSNormGated)
+ *   ds4f_gpu_gqa_prefill  <- the serial gqa_body loop of
+ *                            ds4f_attn_gqa_chunk :1222-1231
+ *   ds4f_gpu_lin_prefill  <- the serial lin_body loop of
+ *                            ds4f_attn_linear_chunk :1088-1109
+ * and the state container they act on is the engine's Ds4fKvCache
+ * (include/ds4f/attn.h:26-42), bound once with ds4f_gpu_attn_bind.
+ *
+ * Activations cross the host ABI as float (the reference's float*), weights
+ * as the raw trunk bits (bf16 as uint16_t, A_log as float).  The device keeps
+ * the KV cache in bf16 (GQA layers only), the delta-rule state in fp32 and
+ * the conv ring in fp32; host arrays are stale until ds4f_gpu_attn_sync.
+ *
+ * Threading: single caller, one HIP stream, static device state (as
+ * src/gpu_metal.mm:16-23).  Calls that overlap race.
+ */
+#ifndef DS4F_GPU_ATTN_H
+#define DS4F_GPU_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- lifecycle (include/ds4f/gpu.h:22-23) ------------------------------ */
+int  ds4f_gpu_init(void);
+void ds4f_gpu_free(void);
+
+/* Layer kinds, decided by the engine the way ds4f_attn_qwen_step does
+ * (src/attn_qwen.c:1259-1263: q3_q role -> GQA, q3_conv/q3_pqkv -> linear). */
+#define DS4F_LAYER_NONE   0
+#define DS4F_LAYER_LINEAR 1
+#define DS4F_LAYER_GQA    2
+
+/* Geometry, in the reference's terms (src/attn_qwen.c:249-252, :451-453):
+ * GQA q heads = linear key heads = n_heads, GQA kv heads = n_kv_heads,
+ * linear value heads = 16 * n_kv_heads, kd = vd = 128, head_dim = 256. */
+typedef struct Ds4fGpuAttnGeom {
+    int n_layers;    /* Ds4fKvCache.n_layers */
+    int max_tokens;  /* Ds4fKvCache.max_tokens */
+    int n_heads;     /* cfg->n_heads */
+    int n_kv_heads;  /* cfg->n_kv_heads */
+    int head_dim;    /* GQA head dim (krows / kv_heads) */
+    int lin_kd;      /* delta-rule key dim (128) */
+    int lin_vd;      /* delta-rule value dim (128) */
+} Ds4fGpuAttnGeom;
+
+/* Bind the engine's state arrays (the Ds4fKvCache fields kv / lin / conv,
+ * allocated by ds4f_kv_init / _lin_init / _conv_init, src/attn.c:27-91):
+ *   host_kv   [n_layers][max_tokens][2*n_kv_heads*head_dim] or NULL
+ *   host_lin  [n_layers][16*n_kv_heads][lin_kd][lin_vd]     or NULL
+ *   host_conv [n_layers][4][conv_rows]                      or NULL
+ * with conv_rows = 2*n_heads*lin_kd + 16*n_kv_heads*lin_vd.  Allocates the
+ * device mirrors (KV only for GQA layers) and uploads the first
+ * n_kv_tokens cache rows plus the whole lin/conv arrays; NULL arrays start
+ * as zeros on the device.  Rebinding replaces the previous binding. */
+int ds4f_gpu_attn_bind(const Ds4fGpuAttnGeom *geom, const int *layer_kind,
+                       float *host_kv, float *host_lin, float *host_conv,
+                       int n_kv_tokens);
+int ds4f_gpu_attn_unbind(void);
+
+/* Move state between the device mirrors and the bound host arrays.
+ * L = -1: every layer.  n_kv_tokens: cache rows [0, n) to move. */
+#define DS4F_SYNC_TO_HOST   0
+#define DS4F_SYNC_TO_DEVICE 1
+int ds4f_gpu_attn_sync(int L, int dir, int n_kv_tokens);
+
+/* ---- host-pointer entry points (synchronous on return) ---------------- */
+
+/* One decode token of a GQA layer (gqa_body :279-396).
+ *   q_gate   [n_heads][2*head_dim]  (q | gate per head)
+ *   k        [n_kv_heads][head_dim] normed + rotated in place, as the
+ *            reference mutates its k (:292-293, :317-325)
+ *   v        [n_kv_heads][head_dim]
+ *   attn_out [n_heads][head_dim]
+ * token >= max_tokens or < 0 is the reference's silent skip (:256):
+ * returns 0 with nothing written. */
+int ds4f_gpu_gqa_decode(int L, int token, const float *q_gate, float *k,
+                        const float *v, const uint16_t *qn_w,
+                        const uint16_t *kn_w, float *attn_out);
+
+/* One decode token of a gated delta-rule layer (lin_body :470-764).
+ *   qkv  [conv_rows] raw projection in; post-conv, normed values out
+ *        (the reference mutates it in place: :503, :535)
+ *   z    [16*n_kv_heads*lin_vd]; a, b [16*n_kv_heads] (in_proj_a/b outputs)
+ *   out  [16*n_kv_heads*lin_vd] gated normed readout (the o_proj input) */
+int ds4f_gpu_lin_decode(int L, int token, float *qkv, const float *z,
+                        const float *a, const float *b,
+                        const uint16_t *conv_w, const float *A_log,
+                        const uint16_t *dt_bias, const uint16_t *norm_w,
+                        float *out);
+
+/* Prefill of B tokens t0..t0+B-1 of a GQA layer: the same results as B
+ * ds4f_gpu_gqa_decode calls in order.  Arrays are [B][...] of the decode
+ * shapes. */
+int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k,
+                         const float *v, const uint16_t *qn_w,
+                         const uint16_t *kn_w, float *attn_out);
+
+/* Prefill of B tokens of a delta-rule layer: the same results as B
+ * ds4f_gpu_lin_decode calls in order (chunked form on the device). */
+int ds4f_gpu_lin_prefill(int L, int t0, int B, float *qkv, const float *z,
+                         const float *a, const float *b,
+                         const uint16_t *conv_w, const float *A_log,
+                         const uint16_t *dt_bias, const uint16_t *norm_w,
+                         float *out);
+
+/* ---- device-pointer entry points (enqueue only) ----------------------- *
+ * The same operations with every tensor already in device memory; they
+ * enqueue on `stream` (a hipStream_t; NULL = the plugin's stream) and
+ * return without waiting, so a caller can keep inputs resident in HBM and
+ * capture the launches in a HIP graph.  k_post / qkv_post may be NULL. */
+int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate,
+                              const float *k, const float *v,
+                              const uint16_t *qn_w, const uint16_t *kn_w,
+                              float *attn_out, float *k_post, void *stream);
+int ds4f_hip_lin_decode_async(int L, int token, const float *qkv,
+                              const float *z, const float *a, const float *b,
+                              const uint16_t *conv_w, const float *A_log,
+                              const uint16_t *dt_bias, const uint16_t *norm_w,
+                              float *out, float *qkv_post, void *stream);
+
+/* ---- synthetic state for benchmarks and tests ------------------------- *
+ * Fill device memory with the splitmix64 / Box-Muller streams of the
+ * workload generator (seed, tensor id; index = logical element index).
+ * dtype 0 = float32, 1 = bf16; dist 0 = normal(p0 = mean, p1 = sigma),
+ * 1 = uniform(p0 = lo, p1 = hi). */
+int ds4f_hip_synth(void *dst, int64_t n, int dtype, int dist, double p0,
+                   double p1, uint64_t seed, uint64_t tid, void *stream);
+/* Bound GQA layer L: cache rows [0, n_past) drawn bf16 N(0,1) in the
+ * reference row order [pos][kv_head][dim] (streams tid_k, tid_v). */
+int ds4f_hip_synth_gqa_cache(int L, int n_past, uint64_t seed, uint64_t tid_k,
+                             uint64_t tid_v, void *stream);
+/* Bound linear layer L: state N(0, sigma) in the order [vh][kd][vd]; conv
+ * ring rows of positions token-3..token-1 drawn N(0,1) as [3][conv_rows]. */
+int ds4f_hip_synth_lin_state(int L, double sigma, uint64_t seed, uint64_t tid,
+                             void *stream);
+int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid,
+                                void *stream);
+
+/* Last error text of the plugin (static storage). */
+const char *ds4f_gpu_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DS4F_GPU_ATTN_H */
