@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Benchmark: decode of the 40-layer Qwen3.5 hybrid attention stack at 32K
+context on one MI355X.
+
+Workload (the path's headline configuration): 40 layers, full GQA at
+layer % 4 == 3 (10 layers: 16 q / 2 kv heads, head_dim 256, bf16 KV cache of
+`--ctx` past tokens drawn N(0,1)), gated delta rule elsewhere (30 layers:
+16 key / 32 value heads of 128, fp32 state N(0, 0.05), conv ring with 3 past
+rows).  Attention cores only: the post-projection activations of every
+(layer, step) are synthetic N(0,1) tensors, generated on the device before
+the timed region.  One step = one token through all 40 layers at position
+ctx + s; every step is one HIP graph of the 40 layer launches.
+
+Prints one JSON line: tokens/s (value), the whole stack's algorithmic HBM
+rate, the roofline of the dominant kernel (the GQA split-K decode kernel,
+timed with hipEvents around each of its launches for the same K steps)
+and the CPU baseline (the C oracle on the host, one thread, on a bounded
+sample of the same steps).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "disk-qwen35ba3b_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "GQA+delta-rule attn tokens/s and HBM GB/s %peak, decode @32K ctx, 1 GPU"
+
+
+def gqa_split_bytes(n_past: int) -> int:
+    """Algorithmic HBM bytes of one GQA split-K launch: the bf16 K and V rows
+    of n_past positions (2 kv heads x 256 x 2 B x 2), the new bf16 row, the q
+    half of q|gate (16 x 256 fp32), new k/v fp32, norm weights, cos/sin."""
+    return 2048 * n_past + 2048 + 16384 + 4096 + 1024 + 256
+
+
+def gqa_layer_bytes(n_past: int) -> int:
+    """Algorithmic bytes of one GQA decode step (KV + 48,384 B of q|gate,
+    k/v, output, norms, cos/sin)."""
+    return 2048 * n_past + 48384
+
+
+LIN_LAYER_BYTES = 4448960   # state r+w 4 MiB, conv rows/weights, qkv, z, gates, output
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU-baseline sample budget (whole steps, at least one)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (--gpus 1); the multi-GPU sharding "
+              "of the path is a design note, not an implementation", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip import synth as S
+    from ds4f_hip import workloads as W
+    from ds4f_hip.attn import GpuAttention, KvCache, dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    gq, lg = W.GqaGeom(), W.LinGeom()
+    kinds = W.stack_kinds(40)
+    N, K, WU, seed = args.ctx, args.steps, args.warmup, args.seed
+    T = WU + K
+    max_tokens = N + T + 64
+    want_cpu = not args.no_cpu_baseline
+
+    # ---- device state: bind (host arrays only when the CPU baseline needs them)
+    cache = KvCache(40, max_tokens) if want_cpu else None
+    ga = GpuAttention(kinds, max_tokens, cache)
+    for Lr, kd in enumerate(kinds):
+        if kd == 2:
+            L.check(lib.ds4f_hip_synth_gqa_cache(Lr, N, seed, S.tid(S.GQA_KCACHE, Lr),
+                                                 S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
+        else:
+            L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr), None),
+                    "synth state")
+            L.check(lib.ds4f_hip_synth_conv_history(Lr, N, seed, S.tid(S.LIN_CONVSTATE, Lr),
+                                                    None), "synth conv")
+
+    def synth(n, dtype, dist, p0, p1, tid, t=None):
+        if t is None:
+            t = torch.empty(n, dtype=torch.float32 if dtype == 0 else torch.int16, device=dev)
+        L.check(lib.ds4f_hip_synth(dptr(t), n, dtype, dist, p0, p1, seed, tid, None), "synth")
+        return t
+
+    # weights and per-(layer, step) activations, resident in HBM
+    layers = []
+    for Lr, kd in enumerate(kinds):
+        d = {"kind": kd}
+        if kd == 2:
+            d["qn"] = synth(gq.head_dim, 1, 0, 1.0, 0.1, S.tid(S.GQA_QNW, Lr))
+            d["kn"] = synth(gq.head_dim, 1, 0, 1.0, 0.1, S.tid(S.GQA_KNW, Lr))
+            nq, nk = gq.heads * 2 * gq.head_dim, gq.kv_heads * gq.head_dim
+            d["q"] = torch.empty((T, nq), dtype=torch.float32, device=dev)
+            d["k"] = torch.empty((T, nk), dtype=torch.float32, device=dev)
+            d["v"] = torch.empty((T, nk), dtype=torch.float32, device=dev)
+            for s in range(T):
+                pos = N + s
+                synth(nq, 0, 0, 0.0, 1.0, S.tid(S.GQA_QGATE, Lr, pos), d["q"][s])
+                synth(nk, 0, 0, 0.0, 1.0, S.tid(S.GQA_K, Lr, pos), d["k"][s])
+                synth(nk, 0, 0, 0.0, 1.0, S.tid(S.GQA_V, Lr, pos), d["v"][s])
+            d["out"] = torch.empty(gq.heads * gq.head_dim, dtype=torch.float32, device=dev)
+        else:
+            d["cw"] = synth(lg.rows * 4, 1, 0, 0.0, 0.1, S.tid(S.LIN_CONVW, Lr))
+            d["al"] = synth(lg.v_heads, 0, 1, 0.0, 2.7, S.tid(S.LIN_ALOG, Lr))
+            d["dt"] = synth(lg.v_heads, 1, 0, 0.0, 0.1, S.tid(S.LIN_DTB, Lr))
+            d["nw"] = synth(lg.vd, 1, 0, 1.0, 0.1, S.tid(S.LIN_NORMW, Lr))
+            nz = lg.v_heads * lg.vd
+            d["qkv"] = torch.empty((T, lg.rows), dtype=torch.float32, device=dev)
+            d["z"] = torch.empty((T, nz), dtype=torch.float32, device=dev)
+            d["a"] = torch.empty((T, lg.v_heads), dtype=torch.float32, device=dev)
+            d["b"] = torch.empty((T, lg.v_heads), dtype=torch.float32, device=dev)
+            for s in range(T):
+                st = s        # step index of the delta-rule activation streams
+                synth(lg.rows, 0, 0, 0.0, 1.0, S.tid(S.LIN_QKV, Lr, st), d["qkv"][s])
+                synth(nz, 0, 0, 0.0, 1.0, S.tid(S.LIN_Z, Lr, st), d["z"][s])
+                synth(lg.v_heads, 0, 0, 0.0, 1.0, S.tid(S.LIN_A, Lr, st), d["a"][s])
+                synth(lg.v_heads, 0, 0, 0.0, 1.0, S.tid(S.LIN_B, Lr, st), d["b"][s])
+            d["out"] = torch.empty(nz, dtype=torch.float32, device=dev)
+        layers.append(d)
+    torch.cuda.synchronize()
+    if want_cpu:
+        ga.sync(-1, to_host=True, n_kv_tokens=N)       # initial state for the CPU sample
+
+    def launch_step(s, stream):
+        pos = N + s
+        for Lr, d in enumerate(layers):
+            if d["kind"] == 2:
+                rc = lib.ds4f_hip_gqa_decode_async(Lr, pos, dptr(d["q"][s]), dptr(d["k"][s]),
+                                                   dptr(d["v"][s]), dptr(d["qn"]), dptr(d["kn"]),
+                                                   dptr(d["out"]), None, stream)
+            else:
+                rc = lib.ds4f_hip_lin_decode_async(Lr, pos, dptr(d["qkv"][s]), dptr(d["z"][s]),
+                                                   dptr(d["a"][s]), dptr(d["b"][s]),
+                                                   dptr(d["cw"]), dptr(d["al"]), dptr(d["dt"]),
+                                                   dptr(d["nw"]), dptr(d["out"]), None, stream)
+            L.check(rc, f"layer {Lr} step {s}")
+
+    def capture(steps):
+        graphs = []
+        side = torch.cuda.Stream()
+        for s in steps:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                launch_step(s, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            graphs.append(g)
+        return graphs
+
+    graphs = capture(range(T))
+    torch.cuda.synchronize()
+    for s in range(WU):
+        graphs[s].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(WU, T):
+        graphs[s].replay()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    sec = t1 - t0
+    ms_step = sec / K * 1e3
+    tok_s = K / sec
+    alg_bytes = sum(10 * gqa_layer_bytes(N + s) + 30 * LIN_LAYER_BYTES for s in range(WU, T))
+    stack_gbps = alg_bytes / sec / 1e9
+
+    # ---- dominant kernel: the GQA launches of the same K steps again, eagerly,
+    # with a hipEvent pair around every split kernel.  The stream is first
+    # loaded with K graph replays (tens of ms of GPU work) so that the host has
+    # queued all profiled launches before the GPU reaches them: the events then
+    # bracket back-to-back kernels, not host enqueue gaps.
+    L.check(lib.ds4f_hip_profile_begin(), "profile_begin")
+    mean_us, min_us, max_us, nl = ctypes.c_double(), ctypes.c_double(), ctypes.c_double(), \
+        ctypes.c_int()
+    torch.cuda.synchronize()
+    for s in range(WU, T):
+        graphs[s].replay()
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for s in range(WU, T):
+        for Lr, d in enumerate(layers):
+            if d["kind"] == 2:
+                L.check(lib.ds4f_hip_gqa_decode_async(Lr, N + s, dptr(d["q"][s]), dptr(d["k"][s]),
+                                                      dptr(d["v"][s]), dptr(d["qn"]),
+                                                      dptr(d["kn"]), dptr(d["out"]), None, cur),
+                        "profiled gqa")
+    torch.cuda.synchronize()
+    L.check(lib.ds4f_hip_profile_end(ctypes.byref(mean_us), ctypes.byref(min_us),
+                                     ctypes.byref(max_us), ctypes.byref(nl)), "profile_end")
+    del graphs
+    split_bytes = sum(gqa_split_bytes(N + s) for s in range(WU, T)) / K
+    achieved = split_bytes / (mean_us.value * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"gqa_split_decode_ctx{N}_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("bytes_per_launch")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                "kernel": "gqa_split_kernel", "launches": nl.value,
+                "mean_us": round(mean_us.value, 3), "min_us": round(min_us.value, 3),
+                "max_us": round(max_us.value, 3),
+                "bytes_per_launch": int(split_bytes)}
+
+    # ---- CPU baseline: the oracle, one thread, same state and streams
+    cpu = None
+    if want_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        O.lib()
+        wts = {}
+        for Lr, kd in enumerate(kinds):
+            wts[Lr] = W.gqa_weights(gq, seed, Lr) if kd == 2 else W.lin_weights(lg, seed, Lr)
+        done, spent = 0, 0.0
+        while done < 64 and (done == 0 or spent < args.cpu_seconds):
+            s, pos = done, N + done
+            for Lr, kd in enumerate(kinds):
+                if kd == 2:
+                    q, k, v = W.gqa_token(gq, seed, Lr, pos)
+                    c0 = time.perf_counter()
+                    O.gqa_body(cache.kv[Lr], pos, q, k, v, wts[Lr][0], wts[Lr][1], gq.heads,
+                               gq.kv_heads, gq.head_dim)
+                    spent += time.perf_counter() - c0
+                else:
+                    qkv, z, a, b = W.lin_token(lg, seed, Lr, s)
+                    w = wts[Lr]
+                    c0 = time.perf_counter()
+                    O.lin_body(cache.conv[Lr], cache.lin[Lr], pos, qkv, z, a, b, w.conv_w,
+                               w.A_log, w.dt_bias, w.norm_w, lg.k_heads, lg.v_heads, lg.kd,
+                               lg.vd)
+                    spent += time.perf_counter() - c0
+            done += 1
+        cpu = {"value": round(done / spent, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{done} decode steps of the same 40-layer stack at {N} context "
+                         f"(positions {N}..{N + done - 1}), C oracle gcc -O2, 1 thread, "
+                         f"{spent:.1f} s"}
+
+    ga.close()
+    line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1,
+            "steps": K, "warmup": WU, "ms_per_step": round(ms_step, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16-kv/fp32",
+            "data": "synthetic (splitmix64 streams, seed 0: KV bf16 N(0,1), state N(0,0.05), "
+                    "activations N(0,1))",
+            "config": {"workload": "qwen3.5-35b-a3b attention stack decode: 40 layers "
+                                   "(30 gated delta-rule + 10 GQA 16q/2kv d256), attention "
+                                   "cores only",
+                       "context": N, "layers": 40, "gqa_layers": 10, "delta_layers": 30,
+                       "batch": 1, "graph_per_step": True},
+            "hbm_gbps": round(stack_gbps, 1), "hbm_frac": round(stack_gbps / HBM_PEAK_GBPS, 4),
+            "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -303,9 +303,17 @@ extern "C" int q35_gqa_max_chunks(void) { return MAX_CHUNKS; }
 extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) {
     if (p->heads != p->kv_heads * G || p->n_chunks < 1 || p->n_chunks > MAX_CHUNKS)
         return hipErrorInvalidValue;
+    if (p->ev_begin) {
+        hipError_t e0 = hipEventRecord(p->ev_begin, stream);
+        if (e0 != hipSuccess) return e0;
+    }
     hipLaunchKernelGGL(gqa_split_kernel, dim3(p->n_chunks, p->kv_heads), dim3(NT), 0, stream, *p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (p->ev_end) {
+        e = hipEventRecord(p->ev_end, stream);
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 64), dim3(256), 0, stream, *p);
     return hipGetLastError();
 }
