@@ -12,9 +12,9 @@ the timed region.  One step = one token through all 40 layers at position
 ctx + s; every step is one HIP graph of the 40 layer launches.
 
 Prints one JSON line: tokens/s (value), the whole stack's algorithmic HBM
-rate, the roofline of the dominant kernel (the GQA split-K decode kernel,
-timed with hipEvents around each of its launches for the same K steps)
-and the CPU baseline (the C oracle on the host, one thread, on a bounded
+rate, the roofline of the dominant kernel (the GQA decode: split-K kernel
+plus merge kernel, its 10 x K launches of the same steps replayed as one
+HIP graph between two hipEvents) and the CPU baseline (the C oracle on the host, one thread, on a bounded
 sample of the same steps).
 """
 from __future__ import annotations
@@ -182,41 +182,42 @@ def main() -> int:
     alg_bytes = sum(10 * gqa_layer_bytes(N + s) + 30 * LIN_LAYER_BYTES for s in range(WU, T))
     stack_gbps = alg_bytes / sec / 1e9
 
-    # ---- dominant kernel: the GQA launches of the same K steps again, eagerly,
-    # with a hipEvent pair around every split kernel.  The stream is first
-    # loaded with K graph replays (tens of ms of GPU work) so that the host has
-    # queued all profiled launches before the GPU reaches them: the events then
-    # bracket back-to-back kernels, not host enqueue gaps.
-    L.check(lib.ds4f_hip_profile_begin(), "profile_begin")
-    mean_us, min_us, max_us, nl = ctypes.c_double(), ctypes.c_double(), ctypes.c_double(), \
-        ctypes.c_int()
-    torch.cuda.synchronize()
-    for s in range(WU, T):
-        graphs[s].replay()
-    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    for s in range(WU, T):
-        for Lr, d in enumerate(layers):
-            if d["kind"] == 2:
-                L.check(lib.ds4f_hip_gqa_decode_async(Lr, N + s, dptr(d["q"][s]), dptr(d["k"][s]),
-                                                      dptr(d["v"][s]), dptr(d["qn"]),
-                                                      dptr(d["kn"]), dptr(d["out"]), None, cur),
-                        "profiled gqa")
-    torch.cuda.synchronize()
-    L.check(lib.ds4f_hip_profile_end(ctypes.byref(mean_us), ctypes.byref(min_us),
-                                     ctypes.byref(max_us), ctypes.byref(nl)), "profile_end")
+    # ---- dominant kernel: the GQA decode (split-K kernel + merge kernel) of
+    # the same K steps, all 10 x K launches captured in one HIP graph and
+    # timed with hipEvents around its replay on the launch stream
     del graphs
-    split_bytes = sum(gqa_split_bytes(N + s) for s in range(WU, T)) / K
-    achieved = split_bytes / (mean_us.value * 1e-6) / 1e9
+    gq_graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.graph(gq_graph, stream=side):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for s in range(WU, T):
+            for Lr, d in enumerate(layers):
+                if d["kind"] == 2:
+                    L.check(lib.ds4f_hip_gqa_decode_async(Lr, N + s, dptr(d["q"][s]),
+                                                          dptr(d["k"][s]), dptr(d["v"][s]),
+                                                          dptr(d["qn"]), dptr(d["kn"]),
+                                                          dptr(d["out"]), None, st), "gqa")
+    n_gqa_launch = 10 * K
+    gq_graph.replay()                      # warm
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    gq_graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    gqa_us = ev0.elapsed_time(ev1) * 1e3 / n_gqa_launch
+    del gq_graph
+    gqa_bytes = sum(gqa_layer_bytes(N + s) for s in range(WU, T)) / K
+    achieved = gqa_bytes / (gqa_us * 1e-6) / 1e9
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"gqa_split_decode_ctx{N}_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"gqa_decode_ctx{N}_traffic.json")
     if os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                "kernel": "gqa_split_kernel", "launches": nl.value,
-                "mean_us": round(mean_us.value, 3), "min_us": round(min_us.value, 3),
-                "max_us": round(max_us.value, 3),
-                "bytes_per_launch": int(split_bytes)}
+                "kernel": "gqa decode = gqa_split_kernel + gqa_merge_kernel",
+                "launches": n_gqa_launch, "us_per_launch": round(gqa_us, 3),
+                "bytes_per_launch": int(gqa_bytes)}
 
     # ---- CPU baseline: the oracle, one thread, same state and streams
     cpu = None

@@ -50,13 +50,6 @@ static struct Plugin {
     size_t d_stage_cap, h_stage_cap;
 } P;
 
-/* split-kernel event pairs of ds4f_hip_profile_begin/_end */
-#define PROF_MAX 4096
-static struct Prof {
-    int on, n, created;
-    hipEvent_t ev[2 * PROF_MAX];
-} PR;
-
 static void set_err(const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -382,41 +375,7 @@ int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate, const float
     p.heads = P.g.n_heads;
     p.kv_heads = P.g.n_kv_heads;
     q35_gqa_split(token, &p.chunk, &p.n_chunks);
-    if (PR.on && PR.n < PR.created / 2) {
-        p.ev_begin = PR.ev[2 * PR.n];
-        p.ev_end = PR.ev[2 * PR.n + 1];
-        PR.n++;
-    }
     HIPCHK(q35_gqa_decode(&p, pick(stream)));
-    return 0;
-}
-
-int ds4f_hip_profile_begin(void) {
-    if (ds4f_gpu_init() != 0) return -1;
-    /* all events up front: none is created inside a graph capture */
-    while (PR.created < 2 * PROF_MAX) HIPCHK(hipEventCreate(&PR.ev[PR.created++]));
-    PR.on = 1;
-    PR.n = 0;
-    return 0;
-}
-
-int ds4f_hip_profile_end(double *mean_us, double *min_us, double *max_us, int *launches) {
-    if (!PR.on) return -1;
-    PR.on = 0;
-    double sum = 0.0, mn = 1e30, mx = 0.0;
-    for (int i = 0; i < PR.n; i++) {
-        float ms = 0.0f;
-        HIPCHK(hipEventSynchronize(PR.ev[2 * i + 1]));
-        HIPCHK(hipEventElapsedTime(&ms, PR.ev[2 * i], PR.ev[2 * i + 1]));
-        double us = (double)ms * 1000.0;
-        sum += us;
-        if (us < mn) mn = us;
-        if (us > mx) mx = us;
-    }
-    if (mean_us) *mean_us = PR.n ? sum / PR.n : 0.0;
-    if (min_us) *min_us = PR.n ? mn : 0.0;
-    if (max_us) *max_us = mx;
-    if (launches) *launches = PR.n;
     return 0;
 }
 

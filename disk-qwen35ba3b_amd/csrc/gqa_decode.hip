@@ -10,10 +10,10 @@
  * streams `chunk` cached positions of one kv head and serves all 8 q heads
  * of that kv head from the same K/V bytes:
  *   scores  S[16 pos][16 col] = K[16 pos][256] * Q^T on 16x16x32 bf16 MFMA,
- *           with columns 0-7 holding the bf16 "hi" part of the 8 q heads and
+ *           columns 0-7 holding the bf16 "hi" part of the 8 q heads and
  *           columns 8-15 the "lo" remainder (q = hi + lo to ~2^-16), so the
  *           fp32 q is used at near-fp32 precision; hi + lo are summed with
- *           one lane exchange;
+ *           one DPP lane exchange;
  *   values  O^T[16 dim][16 col] += V^T[16 dim][16 pos] * P^T on 16x16x16
  *           bf16 MFMA, P split the same way (hi | lo columns);
  *   online softmax per wave, the 4 waves merged in LDS, one partial
@@ -23,6 +23,9 @@
  * which also writes the bf16 cache row.
  * Kernel 2 (merge): rescales and sums the P partials of each q head and
  * applies the gate.
+ *
+ * Every global input of the prologue is loaded up front so the workgroup
+ * pays one memory round trip before its main loop, not one per element.
  */
 #include "q35_device.h"
 #include "q35_launch.h"
@@ -31,35 +34,39 @@ namespace {
 
 constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
 constexpr int NT = 256, NW = 4;
-constexpr int MAX_CHUNKS = 128;
-constexpr float SCALE = 0.0625f;   /* 1/sqrtf(256), src/attn_qwen.c:334 */
+constexpr int MAX_CHUNKS = 256;
+constexpr int OS = 9;                 /* sO row stride (8 heads + 1): conflict-free */
+constexpr float SCALE = 0.0625f;      /* 1/sqrtf(256), src/attn_qwen.c:334 */
+#ifndef Q35_GQA_PIPE
+#define Q35_GQA_PIPE 1      /* register buffers per wave (1 or 2) */
+#endif
+#ifndef Q35_GQA_MINW
+#define Q35_GQA_MINW 2      /* waves per SIMD the register budget targets */
+#endif
 
-/* q_norm (RMSNorm, double sum, eps on the mean) + half-split RoPE of one
- * head held as 4 dims per lane (dims 4l..4l+3); returns the 4 values. */
-__device__ __forceinline__ float4 norm_rope_head(float4 x, const uint16_t *w, const float *rope,
-                                                 int lane) {
+/* RMSNorm (double sum of squares, eps on the mean, x / r * w) and
+ * half-split RoPE of one head held as 4 dims per lane (dims 4l..4l+3).
+ * w: the 4 bf16 weights of those dims; c, s: cos / sin of rotary index
+ * (4l & 31) .. +3, used by lanes < 16 only. */
+__device__ __forceinline__ float4 norm_rope_head(float4 x, uint2 w, float4 c, float4 s, int lane) {
 #pragma clang fp contract(off)
     double ss = (double)x.x * x.x + (double)x.y * x.y + (double)x.z * x.z + (double)x.w * x.w;
     ss = q35_wave_sum(ss);
-    float r = sqrtf((float)(ss / (double)D) + 1e-6f);
-    const int d0 = lane * 4;
+    const float r = sqrtf((float)(ss / (double)D) + 1e-6f);
     float v[4] = {x.x, x.y, x.z, x.w};
+    const uint16_t wt[4] = {(uint16_t)(w.x & 0xffff), (uint16_t)(w.x >> 16),
+                            (uint16_t)(w.y & 0xffff), (uint16_t)(w.y >> 16)};
 #pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = v[e] / r * q35_bf2f(w[d0 + e]);
+    for (int e = 0; e < 4; e++) v[e] = v[e] / r * q35_bf2f(wt[e]);
     /* RoPE pairs (i, i+32), i < 32: lanes 0..7 hold i, lanes 8..15 hold i+32 */
-    float pr[4];
+    const float cc[4] = {c.x, c.y, c.z, c.w}, sn[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
-    for (int e = 0; e < 4; e++) pr[e] = __shfl_xor(v[e], 8);
-    if (lane < RD / 4) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            int i = (d0 + e) & (RD / 2 - 1);
-            float c = rope[i], s = rope[RD / 2 + i];
-            if (lane < RD / 8)
-                v[e] = v[e] * c - pr[e] * s;        /* x0*c - x1*s */
-            else
-                v[e] = pr[e] * s + v[e] * c;        /* x0*s + x1*c */
-        }
+    for (int e = 0; e < 4; e++) {
+        const float pr = q35_xor8(v[e]);
+        if (lane < RD / 8)
+            v[e] = v[e] * cc[e] - pr * sn[e];        /* x0*c - x1*s */
+        else if (lane < RD / 4)
+            v[e] = pr * sn[e] + v[e] * cc[e];        /* x0*s + x1*c */
     }
     return make_float4(v[0], v[1], v[2], v[3]);
 }
@@ -82,132 +89,189 @@ __device__ __forceinline__ void load_v(VTile &vt, const uint16_t *base, int lane
         vt.v[dt] = *reinterpret_cast<const s16x4_t *>(base + (dt * 16 + m) * 16 + grp * 4);
 }
 
-__global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
+/* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
+ * into hi | lo columns, P*V on MFMA into acc. */
+__device__ __forceinline__ void attend_tile(const KTile &kt, VTile &vt, const bf16x8_t *sqb,
+                                            int lane, int base, int c1, int grp, bool is_lo,
+                                            float &m_run, float &l_run, f32x4_t (&acc)[16]) {
+    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt.k[kk], sqb[kk * 64 + lane], sc, 0, 0, 0);
+    /* lane holds S[pos 4grp+i][col n]; add the partner column (hi<->lo) */
+    float sv[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float v = sc[i] + q35_xor8(sc[i]);
+        const int pos = base + 4 * grp + i;
+        v = (pos < c1) ? v * SCALE : -INFINITY;
+        sv[i] = v;
+        tmax = fmaxf(tmax, v);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = q35_exp(m_run - m_new);   /* m_run = -inf -> 0 */
+    const bool rescale = __any(m_new != m_run && m_run != -INFINITY);
+    m_run = m_new;
+    s16x4_t pb;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float pv = q35_exp(sv[i] - m_new);
+        psum += pv;
+        uint16_t hi, lo;
+        q35_split_bf16(pv, hi, lo);
+        pb[i] = (short)(is_lo ? lo : hi);
+    }
+    l_run = l_run * alpha + psum;
+    if (rescale) {   /* wave-uniform: skipped while no running max moves */
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) acc[dt] *= alpha;
+    }
+    if (base + 16 > c1) {
+        /* partial tail tile: zero V of masked positions (0 * junk) */
+        const int valid = c1 - base;   /* 1..15 */
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) vt.v[dt][i] = (4 * grp + i >= valid) ? 0 : vt.v[dt][i];
+    }
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++)
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt.v[dt], pb, acc[dt], 0, 0, 0);
+}
+
+template <int PIPE, int MINW>
+__global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
     const int c = blockIdx.x, g = blockIdx.y;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int n_past = p.token;
     const int c0 = c * p.chunk;
     const int c1 = min(c0 + p.chunk, n_past);
     const bool last = (c == p.n_chunks - 1);
+    const int d0 = lane * 4;
 
     __shared__ float sQ[G][D];
-    __shared__ float sO[NW][G][D];
-    __shared__ float sM[NW + 1][G], sL[NW + 1][G];
+    __shared__ bf16x8_t sQb[8 * 64];
+    __shared__ float sO[NW][D * OS];
+    __shared__ float sM[NW + 1][G], sL[NW + 1][G], sF[NW + 1][G];
     __shared__ float sKn[D], sVn[D];
 
-    /* q of heads 8g+2w, 8g+2w+1: norm + RoPE */
+    /* ---- prologue: every input in flight at once ---- */
+    float4 xq[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++)
+        xq[hh] = *reinterpret_cast<const float4 *>(p.q_gate + (size_t)(g * G + 2 * w + hh) * 2 * D +
+                                                   d0);
+    const uint2 wq = *reinterpret_cast<const uint2 *>(p.qn_w + d0);
+    float4 rc = make_float4(1.f, 1.f, 1.f, 1.f), rs = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane < RD / 4) {
+        rc = *reinterpret_cast<const float4 *>(p.rope + (d0 & (RD / 2 - 1)));
+        rs = *reinterpret_cast<const float4 *>(p.rope + RD / 2 + (d0 & (RD / 2 - 1)));
+    }
+    const bool newtok = last && w == 0;
+    float4 xk = make_float4(0.f, 0.f, 0.f, 0.f), xv = xk;
+    uint2 wk = make_uint2(0, 0);
+    if (newtok) {
+        xk = *reinterpret_cast<const float4 *>(p.k_new + (size_t)g * D + d0);
+        xv = *reinterpret_cast<const float4 *>(p.v_new + (size_t)g * D + d0);
+        wk = *reinterpret_cast<const uint2 *>(p.kn_w + d0);
+    }
+
+    /* q of heads 2w, 2w+1 (of this kv head): norm + RoPE, then straight into
+     * the MFMA B-operand layout: entry [kk][lane'] holds 8 bf16 of column
+     * n = lane'&15 (head n&7, hi if n<8 else lo) for dims 32kk + 8*(lane'>>4).
+     * This lane's dims 4l..4l+3 are half of one such entry. */
+    const int kk0 = d0 >> 5, gp0 = (d0 >> 3) & 3, half = (d0 >> 2) & 1;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         const int qh = 2 * w + hh;
-        const float4 x = *reinterpret_cast<const float4 *>(p.q_gate + (size_t)(g * G + qh) * 2 * D +
-                                                           lane * 4);
-        const float4 y = norm_rope_head(x, p.qn_w, p.rope, lane);
-        *reinterpret_cast<float4 *>(&sQ[qh][lane * 4]) = y;
-    }
-    if (last && w == 0) {
-        /* the new token: k_norm + RoPE in fp32, cache row write (bf16) */
-        const float4 x = *reinterpret_cast<const float4 *>(p.k_new + (size_t)g * D + lane * 4);
-        const float4 y = norm_rope_head(x, p.kn_w, p.rope, lane);
-        const float4 vv = *reinterpret_cast<const float4 *>(p.v_new + (size_t)g * D + lane * 4);
-        *reinterpret_cast<float4 *>(&sKn[lane * 4]) = y;
-        *reinterpret_cast<float4 *>(&sVn[lane * 4]) = vv;
-        if (p.k_post) *reinterpret_cast<float4 *>(p.k_post + (size_t)g * D + lane * 4) = y;
-        const float ky[4] = {y.x, y.y, y.z, y.w}, vy[4] = {vv.x, vv.y, vv.z, vv.w};
+        const float4 y = norm_rope_head(xq[hh], wq, rc, rs, lane);
+        *reinterpret_cast<float4 *>(&sQ[qh][d0]) = y;
+        const float yy[4] = {y.x, y.y, y.z, y.w};
+        s16x4_t hv, lv;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            p.kt[q35_k_index(g, p.token, lane * 4 + e, p.t_tiles)] = q35_f2bf(ky[e]);
-            p.vt[q35_v_index(g, p.token, lane * 4 + e, p.t_tiles)] = q35_f2bf(vy[e]);
+            uint16_t hi, lo;
+            q35_split_bf16(yy[e], hi, lo);
+            hv[e] = (short)hi;
+            lv[e] = (short)lo;
+        }
+        s16x4_t *dst_hi = reinterpret_cast<s16x4_t *>(&sQb[kk0 * 64 + qh + 16 * gp0]) + half;
+        s16x4_t *dst_lo = reinterpret_cast<s16x4_t *>(&sQb[kk0 * 64 + qh + 8 + 16 * gp0]) + half;
+        *dst_hi = hv;
+        *dst_lo = lv;
+    }
+    if (newtok) {
+        /* the new token: k_norm + RoPE in fp32, cache row write (bf16) */
+        const float4 y = norm_rope_head(xk, wk, rc, rs, lane);
+        *reinterpret_cast<float4 *>(&sKn[d0]) = y;
+        *reinterpret_cast<float4 *>(&sVn[d0]) = xv;
+        if (p.k_post) *reinterpret_cast<float4 *>(p.k_post + (size_t)g * D + d0) = y;
+        const float ky[4] = {y.x, y.y, y.z, y.w}, vy[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            p.kt[q35_k_index(g, p.token, d0 + e, p.t_tiles)] = q35_f2bf(ky[e]);
+            p.vt[q35_v_index(g, p.token, d0 + e, p.t_tiles)] = q35_f2bf(vy[e]);
         }
     }
     __syncthreads();
 
-    /* Q as the MFMA B operand: column n = lane&15 (head n&7, hi if n<8 else
-     * lo), k-step kk covers dims 32kk + 8*grp .. +8 */
+    /* ---- main loop over 16-position sub-tiles w, w+4, ... of the chunk ---- */
     const int n = lane & 15, grp = lane >> 4, hq = n & 7;
     const bool is_lo = n >= 8;
-    bf16x8_t qb[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            uint16_t hi, lo;
-            q35_split_bf16(sQ[hq][32 * kk + 8 * grp + e], hi, lo);
-            qb[kk][e] = q35_as_bf16(is_lo ? lo : hi);
-        }
-    }
-
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4_t acc[16];
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const int n_sub = (c1 > c0) ? (c1 - c0 + 15) >> 4 : 0;
-    const size_t kv_head_k = (size_t)g * p.t_tiles * (D / 32) * 512;
-    const size_t kv_head_v = (size_t)g * p.t_tiles * D * 16;
-    for (int s = w; s < n_sub; s += NW) {
-        const int base = c0 + 16 * s;
-        const int tile = base >> 4;
-        KTile kt;
-        VTile vt;
-        load_k(kt, p.kt + kv_head_k + (size_t)tile * (D / 32) * 512, lane);
-        load_v(vt, p.vt + kv_head_v + (size_t)tile * D * 16, lane);
-
-        f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++)
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt.k[kk], qb[kk], sc, 0, 0, 0);
-        /* lane holds S[pos 4grp+i][col n]; add the partner column (hi<->lo) */
-        float sv[4];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float v = sc[i] + __shfl_xor(sc[i], 8);
-            const int pos = base + 4 * grp + i;
-            v = (pos < c1) ? v * SCALE : -INFINITY;
-            sv[i] = v;
-            tmax = fmaxf(tmax, v);
+    const uint16_t *kbase = p.kt + (size_t)g * p.t_tiles * (D / 32) * 512 +
+                            (size_t)(c0 >> 4) * (D / 32) * 512;
+    const uint16_t *vbase = p.vt + (size_t)g * p.t_tiles * D * 16 + (size_t)(c0 >> 4) * D * 16;
+    const int n_mine = (n_sub > w) ? (n_sub - w + NW - 1) / NW : 0;
+    KTile ka, kb;
+    VTile va, vb;
+    if (PIPE == 1) {
+        for (int i = 0; i < n_mine; i++) {
+            const int s0 = w + i * NW;
+            load_k(ka, kbase + (size_t)s0 * (D / 32) * 512, lane);
+            load_v(va, vbase + (size_t)s0 * D * 16, lane);
+            attend_tile(ka, va, sQb, lane, c0 + 16 * s0, c1, grp, is_lo, m_run, l_run, acc);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = expf(m_run - m_new);   /* m_run = -inf -> 0 */
-        m_run = m_new;
-        s16x4_t pb;
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float pv = expf(sv[i] - m_new);
-            psum += pv;
-            uint16_t hi, lo;
-            q35_split_bf16(pv, hi, lo);
-            pb[i] = (short)(is_lo ? lo : hi);
+    } else {
+        if (n_mine > 0) {
+            load_k(ka, kbase + (size_t)w * (D / 32) * 512, lane);
+            load_v(va, vbase + (size_t)w * D * 16, lane);
         }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) acc[dt] *= alpha;
-        if (base + 16 > c1) {
-            /* partial tail tile: zero V of masked positions (0 * junk) */
-            const int valid = c1 - base;   /* 1..15 */
-#pragma unroll
-            for (int dt = 0; dt < 16; dt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (4 * grp + i >= valid) vt.v[dt][i] = 0;
+        for (int i = 0; i < n_mine; i += 2) {
+            const int s0 = w + i * NW, s1 = s0 + NW;
+            if (i + 1 < n_mine) {
+                load_k(kb, kbase + (size_t)s1 * (D / 32) * 512, lane);
+                load_v(vb, vbase + (size_t)s1 * D * 16, lane);
+            }
+            attend_tile(ka, va, sQb, lane, c0 + 16 * s0, c1, grp, is_lo, m_run, l_run, acc);
+            if (i + 1 < n_mine) {
+                if (i + 2 < n_mine) {
+                    load_k(ka, kbase + (size_t)(s1 + NW) * (D / 32) * 512, lane);
+                    load_v(va, vbase + (size_t)(s1 + NW) * D * 16, lane);
+                }
+                attend_tile(kb, vb, sQb, lane, c0 + 16 * s1, c1, grp, is_lo, m_run, l_run, acc);
+            }
         }
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt.v[dt], pb, acc[dt], 0, 0, 0);
     }
 
-    /* per-wave partial: reduce l over the 4 lane groups; O hi + lo columns */
+    /* ---- per-wave partial: l over the 4 lane groups; O hi + lo columns ---- */
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float o = acc[dt][i] + __shfl_xor(acc[dt][i], 8);
-            if (!is_lo) sO[w][hq][16 * dt + 4 * grp + i] = o;
+            const float o = acc[dt][i] + q35_xor8(acc[dt][i]);
+            if (!is_lo) sO[w][(16 * dt + 4 * grp + i) * OS + hq] = o;
         }
     }
     if (lane < G) {
@@ -216,10 +280,10 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     }
     if (last && w == 1) {
         /* the new token's score for the 8 heads, fp32 dot products */
-        const float4 kn = *reinterpret_cast<const float4 *>(&sKn[lane * 4]);
+        const float4 kn = *reinterpret_cast<const float4 *>(&sKn[d0]);
 #pragma unroll
         for (int hh = 0; hh < G; hh++) {
-            const float4 q = *reinterpret_cast<const float4 *>(&sQ[hh][lane * 4]);
+            const float4 q = *reinterpret_cast<const float4 *>(&sQ[hh][d0]);
             float d = q.x * kn.x + q.y * kn.y + q.z * kn.z + q.w * kn.w;
             d = q35_wave_sum(d);
             if (lane == hh) {
@@ -230,59 +294,78 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     }
     __syncthreads();
 
-    /* merge the waves (and the new token) of this workgroup */
+    /* ---- merge the waves (and the new token): 8 x 5 factors once ---- */
     const int nsrc = last ? NW + 1 : NW;
     float *po = p.part_o + ((size_t)(g * p.n_chunks + c) * G) * D;
     float *pml = p.part_ml + ((size_t)(g * p.n_chunks + c) * G) * 2;
+    if (t < G) {
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < nsrc; s2++) M = fmaxf(M, sM[s2][t]);
+        float L = 0.0f;
+        for (int s2 = 0; s2 < NW + 1; s2++) {
+            const float f =
+                (s2 >= nsrc || sM[s2][t] == -INFINITY) ? 0.0f : q35_exp(sM[s2][t] - M);
+            sF[s2][t] = f;
+            L += sL[s2][t] * f;
+        }
+        pml[t * 2] = M;
+        pml[t * 2 + 1] = L;
+    }
+    __syncthreads();
     for (int e = t; e < G * D; e += NT) {
         const int hh = e / D, d = e % D;
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < nsrc; s2++) M = fmaxf(M, sM[s2][hh]);
-        float o = 0.0f, L = 0.0f;
-        for (int s2 = 0; s2 < nsrc; s2++) {
-            const float f = (sM[s2][hh] == -INFINITY) ? 0.0f : expf(sM[s2][hh] - M);
-            const float src = (s2 < NW) ? sO[s2][hh][d] : sVn[d];
-            o += src * f;
-            L += sL[s2][hh] * f;
-        }
+        float o = sO[0][d * OS + hh] * sF[0][hh];
+#pragma unroll
+        for (int s2 = 1; s2 < NW; s2++) o += sO[s2][d * OS + hh] * sF[s2][hh];
+        if (last) o += sVn[d] * sF[NW][hh];
         po[e] = o;
-        if (d == 0) {
-            pml[hh * 2] = M;
-            pml[hh * 2 + 1] = L;
-        }
     }
 }
 
-/* merge: grid (heads, D/64), 256 threads = 4 chunk groups x 64 dims */
+/* merge: grid (heads, D/32), 256 threads.  The P chunk weights
+ * exp(m_c - M) are staged in LDS once; each thread then sums the partial
+ * outputs of every 8th chunk for one dim with independent loads. */
 __global__ __launch_bounds__(256) void gqa_merge_kernel(Q35GqaDecode p) {
     const int h = blockIdx.x, g = h / G, hh = h % G;
-    const int t = threadIdx.x, cg = t >> 6, d = blockIdx.y * 64 + (t & 63);
-    __shared__ float sM[4], sL[4], sO[4][64];
-    const float *pml = p.part_ml + ((size_t)g * p.n_chunks * G + hh) * 2;
-    const float *po = p.part_o + ((size_t)g * p.n_chunks * G + hh) * D + d;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int P = p.n_chunks;
+    __shared__ float sw[MAX_CHUNKS];
+    __shared__ float sred[8][32];
+    __shared__ float swave[4];
+    const int cg = t >> 5, dd = t & 31, d = blockIdx.y * 32 + dd;
+    const float *pml = p.part_ml + ((size_t)g * P * G + hh) * 2;
+    const float gate = p.q_gate[(size_t)h * 2 * D + D + d];
 
-    float M = -INFINITY;
-    for (int c = cg; c < p.n_chunks; c += 4) M = fmaxf(M, pml[(size_t)c * G * 2]);
-    M = fmaxf(M, __shfl_xor(M, 1));   /* uniform within the group already */
-    if ((t & 63) == 0) sM[cg] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(sM[0], sM[1]), fmaxf(sM[2], sM[3]));
-    float o = 0.0f, L = 0.0f;
-    for (int c = cg; c < p.n_chunks; c += 4) {
-        const float mc = pml[(size_t)c * G * 2];
-        const float f = (mc == -INFINITY) ? 0.0f : expf(mc - M);
-        L += pml[(size_t)c * G * 2 + 1] * f;
-        o += po[(size_t)c * G * D] * f;
+    float mc = -INFINITY, lc = 0.0f;
+    if (t < P) {
+        mc = pml[(size_t)t * G * 2];
+        lc = pml[(size_t)t * G * 2 + 1];
     }
+    float M = mc;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    if (lane == 0) swave[w] = M;
     __syncthreads();
-    if ((t & 63) == 0) sL[cg] = L;
-    sO[cg][t & 63] = o;
+    M = fmaxf(fmaxf(swave[0], swave[1]), fmaxf(swave[2], swave[3]));
+    const float f = (t < P && mc != -INFINITY) ? q35_exp(mc - M) : 0.0f;
+    if (t < P) sw[t] = f;
+    float L = q35_wave_sum(lc * f);
+    __syncthreads();
+    if (lane == 0) swave[w] = L;
+    __syncthreads();
+    L = (swave[0] + swave[1]) + (swave[2] + swave[3]);
+
+    const float *po = p.part_o + ((size_t)g * P * G + hh) * D + d;
+    float o = 0.0f;
+#pragma unroll 8
+    for (int c = cg; c < P; c += 8) o += po[(size_t)c * G * D] * sw[c];
+    sred[cg][dd] = o;
     __syncthreads();
     if (cg == 0) {
-        const float Lt = (sL[0] + sL[1]) + (sL[2] + sL[3]);
-        const float ot = (sO[0][t] + sO[1][t]) + (sO[2][t] + sO[3][t]);
-        const float gate = p.q_gate[(size_t)h * 2 * D + D + d];
-        p.attn_out[(size_t)h * D + d] = (ot / Lt) * q35_sigmoid(gate);
+        float ot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ot += sred[j][dd];
+        p.attn_out[(size_t)h * D + d] = (ot / L) * q35_sigmoid(gate);
     }
 }
 
@@ -303,17 +386,10 @@ extern "C" int q35_gqa_max_chunks(void) { return MAX_CHUNKS; }
 extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) {
     if (p->heads != p->kv_heads * G || p->n_chunks < 1 || p->n_chunks > MAX_CHUNKS)
         return hipErrorInvalidValue;
-    if (p->ev_begin) {
-        hipError_t e0 = hipEventRecord(p->ev_begin, stream);
-        if (e0 != hipSuccess) return e0;
-    }
-    hipLaunchKernelGGL(gqa_split_kernel, dim3(p->n_chunks, p->kv_heads), dim3(NT), 0, stream, *p);
+    hipLaunchKernelGGL((gqa_split_kernel<Q35_GQA_PIPE, Q35_GQA_MINW>), dim3(p->n_chunks, p->kv_heads),
+                       dim3(NT), 0, stream, *p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (p->ev_end) {
-        e = hipEventRecord(p->ev_end, stream);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 64), dim3(256), 0, stream, *p);
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 32), dim3(256), 0, stream, *p);
     return hipGetLastError();
 }

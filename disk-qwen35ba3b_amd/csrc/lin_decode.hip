@@ -25,23 +25,17 @@ namespace {
 
 constexpr int KD = 128, VD = 128, NT = 1024;
 
-/* Causal conv tap sum + SiLU for one channel (src/attn_qwen.c:493-504):
- * tap k reads position token-3+k (k = 3 is the incoming raw value), taps
+/* Causal conv tap sum + SiLU of one channel (src/attn_qwen.c:493-504): tap k
+ * reads position token-3+k (k = 3 is the incoming raw value, x[3]); taps
  * before position 0 are skipped. */
-__device__ __forceinline__ float conv_silu(const float *ring, int rows, int ch, float raw,
-                                           const uint16_t *w, int token) {
+__device__ __forceinline__ float conv_silu(const float (&x)[4], uint2 wv, int token) {
 #pragma clang fp contract(off)
-    const uint2 wv = *reinterpret_cast<const uint2 *>(w + (size_t)ch * 4);
     const uint16_t wt[4] = {(uint16_t)(wv.x & 0xffff), (uint16_t)(wv.x >> 16),
                             (uint16_t)(wv.y & 0xffff), (uint16_t)(wv.y >> 16)};
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int tp = token - 3 + k;
-        if (tp < 0) continue;
-        float x = (k == 3) ? raw : ring[(size_t)(tp & 3) * rows + ch];
-        acc += x * q35_bf2f(wt[k]);
-    }
+    for (int k = 0; k < 4; k++)
+        if (token - 3 + k >= 0) acc += x[k] * q35_bf2f(wt[k]);
     return acc * q35_sigmoid(acc);
 }
 
@@ -52,18 +46,14 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     const int rows = 2 * p.k_heads * KD + p.v_heads * VD;
     const int tok = p.token;
 
-    /* state slice first: column j, key rows il*16 .. il*16+15 */
+    /* ---- every global input in flight at once ---- */
+    /* state slice: column j, key rows il*16 .. il*16+15 */
     const int j = t >> 3, il = t & 7;
     float4 *sp = reinterpret_cast<float4 *>(p.state + ((size_t)h * VD + j) * KD + il * 16);
     float4 s[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) s[u] = sp[u];
-
-    __shared__ float sq[KD], sk[KD], sv[VD], so[VD];
-    __shared__ double sred[4];
-    __shared__ float sgate[2];
-
-    /* prologue: conv + SiLU of this head's q (t<128), k (t<256), v (t<384) */
+    /* conv inputs of this head's q (t<128), k (t<256), v (t<384) channels */
     int ch = -1, kind = -1;
     if (t < KD) {
         ch = kh * KD + t;
@@ -75,13 +65,41 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         ch = 2 * p.k_heads * KD + h * VD + (t - 2 * KD);
         kind = 2;
     }
+    float xin[4] = {0.f, 0.f, 0.f, 0.f};
+    uint2 wv = make_uint2(0, 0);
+    if (ch >= 0) {
+#pragma unroll
+        for (int k = 0; k < 3; k++)
+            if (tok - 3 + k >= 0) xin[k] = p.ring[(size_t)((tok - 3 + k) & 3) * rows + ch];
+        xin[3] = p.qkv[ch];
+        wv = *reinterpret_cast<const uint2 *>(p.conv_w + (size_t)ch * 4);
+    }
+    float zv = 0.0f;
+    uint16_t nw = 0;
+    if (t < VD) {
+        zv = p.z[h * VD + t];
+        nw = p.norm_w[t];
+    }
+    float ga = 0.f, gb = 0.f, gal = 0.f;
+    uint16_t gdt = 0;
+    if (t == 2 * KD + VD) {
+        ga = p.a[h];
+        gb = p.b[h];
+        gal = p.A_log[h];
+        gdt = p.dt_bias[h];
+    }
+
+    __shared__ float sq[KD], sk[KD], sv[VD], so[VD];
+    __shared__ double sred[4];
+    __shared__ float sgate[2];
+
+    /* ---- prologue: conv + SiLU, ring update, q/k norms, gates ---- */
     float x = 0.0f;
     if (ch >= 0) {
-        const float raw = p.qkv[ch];
-        x = conv_silu(p.ring, rows, ch, raw, p.conv_w, tok);
+        x = conv_silu(xin, wv, tok);
         /* ring slot token%4 takes the raw row; q/k channels are shared by
          * the two value heads of a key head, the even one writes them */
-        if (kind == 2 || (h & 1) == 0) p.ring[(size_t)(tok & 3) * rows + ch] = raw;
+        if (kind == 2 || (h & 1) == 0) p.ring[(size_t)(tok & 3) * rows + ch] = xin[3];
     }
     double ss = (kind == 0 || kind == 1) ? (double)x * x : 0.0;
     ss = q35_wave_sum(ss);
@@ -89,11 +107,11 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     if (t == 2 * KD + VD) {
         /* gates (src/attn_qwen.c:545-551, :664-665) */
 #pragma clang fp contract(off)
-        float xa = p.a[h] + q35_bf2f(p.dt_bias[h]);
+        float xa = ga + q35_bf2f(gdt);
         float sp_ = xa > 0 ? xa + log1pf(expf(-xa)) : log1pf(expf(xa));
-        float g = -expf(p.A_log[h]) * sp_;
+        float g = -expf(gal) * sp_;
         sgate[0] = expf(g);
-        sgate[1] = q35_sigmoid(p.b[h]);
+        sgate[1] = q35_sigmoid(gb);
     }
     __syncthreads();
     if (kind == 0 || kind == 1) {
@@ -115,7 +133,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     }
     __syncthreads();
 
-    /* gated delta rule on column j (src/attn_qwen.c:666-690) */
+    /* ---- gated delta rule on column j (src/attn_qwen.c:666-690) ---- */
     const float dec = sgate[0], beta = sgate[1];
     const float4 *k4 = reinterpret_cast<const float4 *>(sk + il * 16);
     const float4 *q4 = reinterpret_cast<const float4 *>(sq + il * 16);
@@ -154,7 +172,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     if (il == 0) so[j] = o;
     __syncthreads();
 
-    /* RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749) */
+    /* ---- RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749) ---- */
     if (t < VD) {
         double o2 = (double)so[t] * so[t];
         o2 = q35_wave_sum(o2);
@@ -164,9 +182,8 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     if (t < VD) {
 #pragma clang fp contract(off)
         float r = sqrtf((float)((sred[0] + sred[1]) / (double)VD) + 1e-6f);
-        float zv = p.z[h * VD + t];
         float sg = q35_sigmoid(zv);
-        p.out[h * VD + t] = so[t] / r * q35_bf2f(p.norm_w[t]) * (zv * sg);
+        p.out[h * VD + t] = so[t] / r * q35_bf2f(nw) * (zv * sg);
     }
 }
 

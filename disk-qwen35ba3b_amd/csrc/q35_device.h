@@ -20,12 +20,9 @@ __device__ __forceinline__ float q35_bf2f(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
 }
 
-/* float -> bf16 bits, round to nearest even (NaN kept quiet). */
+/* float -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950). */
 __device__ __forceinline__ uint16_t q35_f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 /* hi + lo split of a float into two bf16 (hi = rne(x), lo = rne(x - hi)). */
@@ -38,11 +35,23 @@ __device__ __forceinline__ __bf16 q35_as_bf16(uint16_t h) {
     return __builtin_bit_cast(__bf16, h);
 }
 
+/* value of lane (l ^ 8): a row_ror:8 DPP move inside each 16-lane row */
+__device__ __forceinline__ float q35_xor8(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, true));
+}
+
 template <typename T>
 __device__ __forceinline__ T q35_wave_sum(T v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
+}
+
+/* exp on the hardware 2^x instruction (v_exp_f32), ~1e-7 relative error:
+ * used for softmax weights, whose reference-order expf only matters to
+ * float rounding. */
+__device__ __forceinline__ float q35_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
 /* sigmoid written as the reference writes it: 1 / (1 + expf(-x)). */

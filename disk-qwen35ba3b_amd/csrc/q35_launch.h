@@ -53,7 +53,6 @@ typedef struct Q35GqaDecode {
     int t_tiles;                   /* T/16 of this layer's tiles */
     int heads, kv_heads;
     int chunk, n_chunks;           /* positions per workgroup, P */
-    hipEvent_t ev_begin, ev_end;   /* optional: recorded around the split kernel */
 } Q35GqaDecode;
 hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream);
 /* P and chunk for a step with n_past cached rows. */

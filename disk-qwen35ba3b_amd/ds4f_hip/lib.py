@@ -49,9 +49,6 @@ _SIGS = {
     "ds4f_hip_synth_gqa_cache": ([_i, _i, _u64, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_lin_state": ([_i, _d, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_conv_history": ([_i, _i, _u64, _u64, _vp], _i),
-    "ds4f_hip_profile_begin": ([], _i),
-    "ds4f_hip_profile_end": ([ctypes.POINTER(_d), ctypes.POINTER(_d), ctypes.POINTER(_d),
-                              ctypes.POINTER(_i)], _i),
     "ds4f_gpu_last_error": ([], ctypes.c_char_p),
 }
 

@@ -157,14 +157,6 @@ int ds4f_hip_synth_lin_state(int L, double sigma, uint64_t seed, uint64_t tid,
 int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid,
                                 void *stream);
 
-/* ---- kernel timing (diagnostics; no counterpart in the reference) ------ *
- * Between begin and end, every GQA decode records a hipEvent pair around its
- * split-K kernel on the launch stream (also inside a HIP graph capture, where
- * the records become graph nodes).  end() waits for the events and returns
- * the mean / min / max kernel time in microseconds and the launch count. */
-int ds4f_hip_profile_begin(void);
-int ds4f_hip_profile_end(double *mean_us, double *min_us, double *max_us, int *launches);
-
 /* Last error text of the plugin (static storage). */
 const char *ds4f_gpu_last_error(void);
 
