@@ -322,49 +322,55 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
     }
 }
 
-/* merge: grid (heads, D/32), 256 threads.  The P chunk weights
- * exp(m_c - M) are staged in LDS once; each thread then sums the partial
- * outputs of every 8th chunk for one dim with independent loads. */
+/* merge: grid (heads, D/16), 256 threads = 16 chunk groups x 16 dims.  All
+ * partial loads of a thread (up to MAX_CHUNKS/16, fully unrolled) and the
+ * chunk maxima / sums are issued together: one memory round trip. */
+constexpr int MG = 16;                          /* chunk groups */
+constexpr int MPER = MAX_CHUNKS / MG;           /* chunks per thread, at most */
 __global__ __launch_bounds__(256) void gqa_merge_kernel(Q35GqaDecode p) {
     const int h = blockIdx.x, g = h / G, hh = h % G;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int P = p.n_chunks;
-    __shared__ float sw[MAX_CHUNKS];
-    __shared__ float sred[8][32];
-    __shared__ float swave[4];
-    const int cg = t >> 5, dd = t & 31, d = blockIdx.y * 32 + dd;
+    __shared__ float sred[MG][16];
+    __shared__ float swave[2][4];
+    const int cg = t >> 4, dd = t & 15, d = blockIdx.y * 16 + dd;
     const float *pml = p.part_ml + ((size_t)g * P * G + hh) * 2;
-    const float gate = p.q_gate[(size_t)h * 2 * D + D + d];
+    const float *po = p.part_o + ((size_t)g * P * G + hh) * D + d;
 
     float mc = -INFINITY, lc = 0.0f;
     if (t < P) {
         mc = pml[(size_t)t * G * 2];
         lc = pml[(size_t)t * G * 2 + 1];
     }
+    float ov[MPER], mv[MPER];
+#pragma unroll
+    for (int j = 0; j < MPER; j++) {
+        const int c = cg + MG * j;
+        ov[j] = (c < P) ? po[(size_t)c * G * D] : 0.0f;
+        mv[j] = (c < P) ? pml[(size_t)c * G * 2] : -INFINITY;
+    }
+    const float gate = p.q_gate[(size_t)h * 2 * D + D + d];
+
     float M = mc;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    if (lane == 0) swave[w] = M;
+    if (lane == 0) swave[0][w] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(swave[0], swave[1]), fmaxf(swave[2], swave[3]));
-    const float f = (t < P && mc != -INFINITY) ? q35_exp(mc - M) : 0.0f;
-    if (t < P) sw[t] = f;
-    float L = q35_wave_sum(lc * f);
-    __syncthreads();
-    if (lane == 0) swave[w] = L;
-    __syncthreads();
-    L = (swave[0] + swave[1]) + (swave[2] + swave[3]);
-
-    const float *po = p.part_o + ((size_t)g * P * G + hh) * D + d;
+    M = fmaxf(fmaxf(swave[0][0], swave[0][1]), fmaxf(swave[0][2], swave[0][3]));
+    const float f = (mc != -INFINITY) ? q35_exp(mc - M) : 0.0f;
+    const float L0 = q35_wave_sum(lc * f);
+    if (lane == 0) swave[1][w] = L0;
     float o = 0.0f;
-#pragma unroll 8
-    for (int c = cg; c < P; c += 8) o += po[(size_t)c * G * D] * sw[c];
+#pragma unroll
+    for (int j = 0; j < MPER; j++)
+        if (mv[j] != -INFINITY) o += ov[j] * q35_exp(mv[j] - M);
     sred[cg][dd] = o;
     __syncthreads();
     if (cg == 0) {
+        const float L = (swave[1][0] + swave[1][1]) + (swave[1][2] + swave[1][3]);
         float ot = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) ot += sred[j][dd];
+        for (int k = 0; k < MG; k++) ot += sred[k][dd];
         p.attn_out[(size_t)h * D + d] = (ot / L) * q35_sigmoid(gate);
     }
 }
@@ -372,7 +378,10 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(Q35GqaDecode p) {
 }  // namespace
 
 extern "C" void q35_gqa_split(int n_past, int *chunk, int *n_chunks) {
-    int per = (n_past + MAX_CHUNKS - 1) / MAX_CHUNKS;
+    /* about 128 chunks per kv head (256 workgroups); chunks are multiples of
+     * 64 positions (4 sub-tiles per wave at least) */
+    const int target = 128;
+    int per = (n_past + target - 1) / target;
     int ch = ((per + 63) / 64) * 64;
     if (ch < 64) ch = 64;
     int P = (n_past + ch - 1) / ch;
@@ -390,6 +399,6 @@ extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) 
                        dim3(NT), 0, stream, *p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 32), dim3(256), 0, stream, *p);
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 16), dim3(256), 0, stream, *p);
     return hipGetLastError();
 }

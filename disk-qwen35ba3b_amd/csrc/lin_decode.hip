@@ -147,9 +147,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         mem = fmaf(s[u].z, kk.z, mem);
         mem = fmaf(s[u].w, kk.w, mem);
     }
-    mem += __shfl_xor(mem, 4);
-    mem += __shfl_xor(mem, 2);
-    mem += __shfl_xor(mem, 1);
+    mem = q35_sum8(mem);      /* the 8 lanes of column j */
     const float delta = (sv[j] - mem) * beta;
     float o = 0.0f;
 #pragma unroll
@@ -164,9 +162,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         o = fmaf(s[u].z, qq.z, o);
         o = fmaf(s[u].w, qq.w, o);
     }
-    o += __shfl_xor(o, 4);
-    o += __shfl_xor(o, 2);
-    o += __shfl_xor(o, 1);
+    o = q35_sum8(o);
 #pragma unroll
     for (int u = 0; u < 4; u++) sp[u] = s[u];
     if (il == 0) so[j] = o;

@@ -35,16 +35,51 @@ __device__ __forceinline__ __bf16 q35_as_bf16(uint16_t h) {
     return __builtin_bit_cast(__bf16, h);
 }
 
-/* value of lane (l ^ 8): a row_ror:8 DPP move inside each 16-lane row */
-__device__ __forceinline__ float q35_xor8(float x) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, true));
+/* DPP lane moves (VALU-latency, no LDS round trip).  Controls used:
+ * quad_perm [1,0,3,2] = 0xB1 (lane ^ 1), quad_perm [2,3,0,1] = 0x4E
+ * (lane ^ 2), row_half_mirror = 0x141 (i <-> 7-i in each 8 lanes),
+ * row_mirror = 0x140 (i <-> 15-i in each 16 lanes), row_ror:8 = 0x128. */
+template <int CTRL>
+__device__ __forceinline__ float q35_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ double q35_dpp(double x) {
+    const long long b = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_mov_dpp((int)(b & 0xffffffff), CTRL, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xF, 0xF, true);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
+/* value of lane (l ^ 8) inside each 16-lane row */
+__device__ __forceinline__ float q35_xor8(float x) { return q35_dpp<0x128>(x); }
+
+/* sum over each aligned group of 8 lanes, the total in every lane of it */
+template <typename T>
+__device__ __forceinline__ T q35_sum8(T v) {
+    v += q35_dpp<0xB1>(v);
+    v += q35_dpp<0x4E>(v);
+    v += q35_dpp<0x141>(v);
+    return v;
+}
+
+__device__ __forceinline__ float q35_readlane(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double q35_readlane(double v, int l) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffff), l);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+/* sum over the 64 lanes of a wave, the total in every lane: 16-lane rows on
+ * DPP, then the four row totals through readlane */
 template <typename T>
 __device__ __forceinline__ T q35_wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = q35_sum8(v);
+    v += q35_dpp<0x140>(v);
+    return (q35_readlane(v, 0) + q35_readlane(v, 16)) + (q35_readlane(v, 32) + q35_readlane(v, 48));
 }
 
 /* exp on the hardware 2^x instruction (v_exp_f32), ~1e-7 relative error:
