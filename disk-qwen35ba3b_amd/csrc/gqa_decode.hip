@@ -79,14 +79,16 @@ __device__ __forceinline__ void load_k(KTile &kt, const uint16_t *base, int lane
     const int m = lane & 15, grp = lane >> 4;
 #pragma unroll
     for (int kk = 0; kk < 8; kk++)
-        kt.k[kk] = *reinterpret_cast<const bf16x8_t *>(base + kk * 512 + m * 32 + grp * 8);
+        kt.k[kk] = __builtin_nontemporal_load(
+            reinterpret_cast<const bf16x8_t *>(base + kk * 512 + m * 32 + grp * 8));
 }
 __device__ __forceinline__ void load_v(VTile &vt, const uint16_t *base, int lane) {
     /* base: the tile's [256 dim][16 tok] block; dims 16dt.. at +dt*256 */
     const int m = lane & 15, grp = lane >> 4;
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
-        vt.v[dt] = *reinterpret_cast<const s16x4_t *>(base + (dt * 16 + m) * 16 + grp * 4);
+        vt.v[dt] = __builtin_nontemporal_load(
+            reinterpret_cast<const s16x4_t *>(base + (dt * 16 + m) * 16 + grp * 4));
 }
 
 /* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
