@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
-"""Benchmark: decode of the 40-layer Qwen3.5 hybrid attention stack at 32K
-context on one MI355X.
+"""Benchmark of the Qwen3.5 hybrid-attention hot path on one MI355X.
 
-Workload (the path's headline configuration): 40 layers, full GQA at
+Default workload (--workload stack_decode, the path's headline
+configuration): 40 layers, full GQA at
 layer % 4 == 3 (10 layers: 16 q / 2 kv heads, head_dim 256, bf16 KV cache of
 `--ctx` past tokens drawn N(0,1)), gated delta rule elsewhere (30 layers:
 16 key / 32 value heads of 128, fp32 state N(0, 0.05), conv ring with 3 past
@@ -14,8 +14,12 @@ ctx + s; every step is one HIP graph of the 40 layer launches.
 Prints one JSON line: tokens/s (value), the whole stack's algorithmic HBM
 rate, the roofline of the dominant kernel (the GQA decode: split-K kernel
 plus merge kernel, its 10 x K launches of the same steps replayed as one
-HIP graph between two hipEvents) and the CPU baseline (the C oracle on the host, one thread, on a bounded
-sample of the same steps).
+HIP graph between two hipEvents) and the CPU baseline (the C oracle on the
+host, one thread, on a bounded sample of the same steps).
+
+Other workloads (one JSON line each, same fields):
+  gqa_prefill   causal GQA prefill of --tokens (4096) tokens, one layer,
+                bf16-valued q|gate/k/v N(0,1); MFMA roofline.
 """
 from __future__ import annotations
 
@@ -30,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "disk-qwen35ba3b_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0     # dense bf16 / fp16
 METRIC = "GQA+delta-rule attn tokens/s and HBM GB/s %peak, decode @32K ctx, 1 GPU"
 
 
@@ -59,13 +64,20 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU-baseline sample budget (whole steps, at least one)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill"])
+    ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (--gpus 1); the multi-GPU sharding "
               "of the path is a design note, not an implementation", file=sys.stderr)
         return 2
+    if args.workload == "gqa_prefill":
+        return run_gqa_prefill(args)
+    return run_stack_decode(args)
 
+
+def run_stack_decode(args) -> int:
     import numpy as np
     import torch
 
@@ -265,6 +277,104 @@ def main() -> int:
                        "context": N, "layers": 40, "gqa_layers": 10, "delta_layers": 30,
                        "batch": 1, "graph_per_step": True},
             "hbm_gbps": round(stack_gbps, 1), "hbm_frac": round(stack_gbps / HBM_PEAK_GBPS, 4),
+            "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_gqa_prefill(args) -> int:
+    """One causal GQA prefill of T tokens (one layer, t0 = 0) per step."""
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip import synth as S
+    from ds4f_hip import workloads as W
+    from ds4f_hip.attn import GpuAttention, dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    gq = W.GqaGeom()
+    T, K, WU, seed = args.tokens, max(1, min(args.steps, 50)), max(1, min(args.warmup, 5)), args.seed
+    ga = GpuAttention([2], T + 64, None)
+    nq, nk = gq.heads * 2 * gq.head_dim, gq.kv_heads * gq.head_dim
+    q = torch.empty((T, nq), dtype=torch.float32, device=dev)
+    k = torch.empty((T, nk), dtype=torch.float32, device=dev)
+    v = torch.empty((T, nk), dtype=torch.float32, device=dev)
+    for t in range(T):     # bf16-valued N(0,1) inputs, per-token streams
+        L.check(lib.ds4f_hip_synth(dptr(q[t]), nq, 2, 0, 0.0, 1.0, seed,
+                                   S.tid(S.GQA_QGATE, 0, t), None), "synth")
+        L.check(lib.ds4f_hip_synth(dptr(k[t]), nk, 2, 0, 0.0, 1.0, seed, S.tid(S.GQA_K, 0, t),
+                                   None), "synth")
+        L.check(lib.ds4f_hip_synth(dptr(v[t]), nk, 2, 0, 0.0, 1.0, seed, S.tid(S.GQA_V, 0, t),
+                                   None), "synth")
+    qn = torch.empty(gq.head_dim, dtype=torch.int16, device=dev)
+    kn = torch.empty(gq.head_dim, dtype=torch.int16, device=dev)
+    L.check(lib.ds4f_hip_synth(dptr(qn), gq.head_dim, 1, 0, 1.0, 0.1, seed, S.tid(S.GQA_QNW, 0),
+                               None), "synth")
+    L.check(lib.ds4f_hip_synth(dptr(kn), gq.head_dim, 1, 0, 1.0, 0.1, seed, S.tid(S.GQA_KNW, 0),
+                               None), "synth")
+    out = torch.empty((T, gq.heads * gq.head_dim), dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()          # a real stream: events and launches share it
+    torch.cuda.set_stream(stream)
+    st = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        L.check(lib.ds4f_hip_gqa_prefill_async(0, 0, T, dptr(q), dptr(k), dptr(v), dptr(qn),
+                                               dptr(kn), dptr(out), None, st), "gqa prefill")
+
+    for _ in range(WU):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(K):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    op_us = ev0.elapsed_time(ev1) * 1e3 / K
+    flops = 4.0 * gq.heads * gq.head_dim * T * (T + 1) / 2
+    tflops = flops / (op_us * 1e-6) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "gqa prefill = prep_kernel + prefix_kernel + attn_kernel (fp16 MFMA)",
+                "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the reference prefill is T serial gqa_body calls; time the body at
+        # sampled positions on the same inputs and integrate the linear fit
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import numpy as np
+        import oracle as O
+        qn_h, kn_h = W.gqa_weights(gq, seed, 0)
+        pos = np.linspace(0, T - 1, 9).astype(int)
+        hq, hk, hv = W.gqa_prefill_tokens(gq, int(pos.max()) + 1, seed, 0)
+        rows = O.gqa_cache_rows(hk, hv, kn_h, 0, gq.kv_heads, gq.head_dim)
+        kv = np.zeros((T, 2 * gq.kv_heads * gq.head_dim), np.float32)
+        kv[:rows.shape[0]] = rows
+        secs = []
+        for t in pos:
+            c0 = time.perf_counter()
+            O.gqa_body(kv, int(t), hq[t].reshape(-1), hk[t].reshape(-1), hv[t].reshape(-1), qn_h,
+                       kn_h, gq.heads, gq.kv_heads, gq.head_dim)
+            secs.append(time.perf_counter() - c0)
+        a, b = np.polyfit(pos.astype(float), np.array(secs), 1)
+        est = float(sum(a * t + b for t in range(T)))
+        cpu = {"value": round(T / est, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"oracle gqa_body timed at {len(pos)} positions 0..{T - 1} of the same "
+                         f"prefill ({sum(secs):.1f} s), linear fit integrated over the "
+                         f"{T} serial calls the reference makes (est. {est:.1f} s)"}
+    ga.close()
+    line = {"metric": f"GQA causal prefill tokens/s ({T} tokens, 16q/2kv d256, 1 layer)",
+            "value": round(T / (op_us * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+            "warmup": WU, "ms_per_step": round(op_us / 1e3, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp16-mfma/fp32",
+            "data": "synthetic (splitmix64 streams, seed 0: bf16-valued q|gate, k, v N(0,1))",
+            "config": {"workload": "gqa causal prefill", "tokens": T, "t0": 0, "layers": 1},
+            "wall_ms_per_step": round(sec / K * 1e3, 4),
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0

@@ -48,6 +48,8 @@ static struct Plugin {
 
     void *d_stage, *h_stage;
     size_t d_stage_cap, h_stage_cap;
+    void *d_ws;                /* prefill workspaces (grow-only) */
+    size_t ws_cap;
 } P;
 
 static void set_err(const char *fmt, ...) {
@@ -119,6 +121,7 @@ void ds4f_gpu_free(void) {
     free_binding();
     if (P.d_stage) hipFree(P.d_stage);
     if (P.h_stage) hipHostFree(P.h_stage);
+    if (P.d_ws) hipFree(P.d_ws);
     hipStreamDestroy(P.stream);
     memset(&P, 0, sizeof P);
 }
@@ -145,6 +148,19 @@ static int ensure_stage(size_t dbytes, size_t hbytes) {
         HIPCHK(hipHostMalloc(&P.h_stage, hbytes, 0));
         P.h_stage_cap = hbytes;
     }
+    return 0;
+}
+
+static int ensure_ws(size_t bytes) {
+    if (bytes <= P.ws_cap) return 0;
+    if (P.d_ws) {
+        HIPCHK(hipStreamSynchronize(P.stream));
+        hipFree(P.d_ws);
+    }
+    P.d_ws = NULL;
+    P.ws_cap = 0;
+    HIPCHK(hipMalloc(&P.d_ws, bytes));
+    P.ws_cap = bytes;
     return 0;
 }
 
@@ -379,6 +395,39 @@ int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate, const float
     return 0;
 }
 
+int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate, const float *k,
+                               const float *v, const uint16_t *qn_w, const uint16_t *kn_w,
+                               float *attn_out, float *k_post, void *stream) {
+    if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
+    if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;   /* src/attn_qwen.c:256 */
+    if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
+    size_t qb, kb, vb;
+    q35_gqa_prefill_ws_bytes(t0, B, P.g.n_kv_heads, &qb, &kb, &vb);
+    if (ensure_ws(qb + kb + vb) != 0) return -1;
+    Q35GqaPrefill p;
+    memset(&p, 0, sizeof p);
+    p.q_gate = q_gate;
+    p.k_in = k;
+    p.v_in = v;
+    p.qn_w = qn_w;
+    p.kn_w = kn_w;
+    p.rope = P.d_rope;
+    p.kt = layer_k(P.slot[L]);
+    p.vt = layer_v(P.slot[L]);
+    p.qw = (uint16_t *)P.d_ws;
+    p.kw = (uint16_t *)((char *)P.d_ws + qb);
+    p.vw = (uint16_t *)((char *)P.d_ws + qb + kb);
+    p.attn_out = attn_out;
+    p.k_post = k_post;
+    p.t0 = t0;
+    p.B = B;
+    p.t_tiles = P.t_tiles;
+    p.heads = P.g.n_heads;
+    p.kv_heads = P.g.n_kv_heads;
+    HIPCHK(q35_gqa_prefill(&p, pick(stream)));
+    return 0;
+}
+
 int ds4f_hip_lin_decode_async(int L, int token, const float *qkv, const float *z, const float *a,
                               const float *b, const uint16_t *conv_w, const float *A_log,
                               const uint16_t *dt_bias, const uint16_t *norm_w, float *out,
@@ -491,20 +540,30 @@ int ds4f_gpu_lin_decode(int L, int token, float *qkv, const float *z, const floa
     return 0;
 }
 
-/* Prefill over B tokens.  The device prefill kernels are in
- * gqa_prefill.hip / lin_prefill.hip; until a layer shape is covered by
- * them the token loop below runs the decode kernels in order, which gives
- * the serial semantics of src/attn_qwen.c:1222-1231 / :1088-1109. */
+/* Prefill over B tokens (src/attn_qwen.c:1222-1231 / :1088-1109 semantics). */
 int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k, const float *v,
                          const uint16_t *qn_w, const uint16_t *kn_w, float *attn_out) {
     if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
+    if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;
+    if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;   /* later tokens: silent skip */
+    if (forced_failure()) return fail_over(t0);
     const int H = P.g.n_heads, KVH = P.g.n_kv_heads, D = GQA_D;
-    for (int t = 0; t < B; t++) {
-        int rc = ds4f_gpu_gqa_decode(L, t0 + t, q_gate + (size_t)t * H * 2 * D,
-                                     k + (size_t)t * KVH * D, v + (size_t)t * KVH * D, qn_w,
-                                     kn_w, attn_out + (size_t)t * H * D);
-        if (rc != 0) return rc;
-    }
+    void *dq, *dk, *dv, *dqn, *dkn, *dout;
+    Piece pc[5] = {{q_gate, (size_t)B * H * 2 * D * 4, &dq},
+                   {k, (size_t)B * KVH * D * 4, &dk},
+                   {v, (size_t)B * KVH * D * 4, &dv},
+                   {qn_w, (size_t)D * 2, &dqn},
+                   {kn_w, (size_t)D * 2, &dkn}};
+    const size_t ob = (size_t)B * H * D * 4, kb = (size_t)B * KVH * D * 4;
+    if (upload(pc, 5, ob + kb, &dout) != 0) return fail_over(t0);
+    float *d_attn = (float *)dout, *d_kpost = (float *)((char *)dout + ob);
+    if (ds4f_hip_gqa_prefill_async(L, t0, B, (const float *)dq, (const float *)dk,
+                                   (const float *)dv, (const uint16_t *)dqn,
+                                   (const uint16_t *)dkn, d_attn, d_kpost, NULL) != 0 ||
+        download(dout, ob + kb) != 0)
+        return fail_over(t0 + B);
+    memcpy(attn_out, P.h_stage, ob);
+    memcpy(k, (char *)P.h_stage + ob, kb);
     return 0;
 }
 

@@ -44,33 +44,6 @@ constexpr float SCALE = 0.0625f;      /* 1/sqrtf(256), src/attn_qwen.c:334 */
 #define Q35_GQA_MINW 2      /* waves per SIMD the register budget targets */
 #endif
 
-/* RMSNorm (double sum of squares, eps on the mean, x / r * w) and
- * half-split RoPE of one head held as 4 dims per lane (dims 4l..4l+3).
- * w: the 4 bf16 weights of those dims; c, s: cos / sin of rotary index
- * (4l & 31) .. +3, used by lanes < 16 only. */
-__device__ __forceinline__ float4 norm_rope_head(float4 x, uint2 w, float4 c, float4 s, int lane) {
-#pragma clang fp contract(off)
-    double ss = (double)x.x * x.x + (double)x.y * x.y + (double)x.z * x.z + (double)x.w * x.w;
-    ss = q35_wave_sum(ss);
-    const float r = sqrtf((float)(ss / (double)D) + 1e-6f);
-    float v[4] = {x.x, x.y, x.z, x.w};
-    const uint16_t wt[4] = {(uint16_t)(w.x & 0xffff), (uint16_t)(w.x >> 16),
-                            (uint16_t)(w.y & 0xffff), (uint16_t)(w.y >> 16)};
-#pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = v[e] / r * q35_bf2f(wt[e]);
-    /* RoPE pairs (i, i+32), i < 32: lanes 0..7 hold i, lanes 8..15 hold i+32 */
-    const float cc[4] = {c.x, c.y, c.z, c.w}, sn[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float pr = q35_xor8(v[e]);
-        if (lane < RD / 8)
-            v[e] = v[e] * cc[e] - pr * sn[e];        /* x0*c - x1*s */
-        else if (lane < RD / 4)
-            v[e] = pr * sn[e] + v[e] * cc[e];        /* x0*s + x1*c */
-    }
-    return make_float4(v[0], v[1], v[2], v[3]);
-}
-
 struct KTile { bf16x8_t k[8]; };
 struct VTile { s16x4_t v[16]; };
 
@@ -190,7 +163,7 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
         const int qh = 2 * w + hh;
-        const float4 y = norm_rope_head(xq[hh], wq, rc, rs, lane);
+        const float4 y = q35_norm_rope_head(xq[hh], wq, rc, rs, lane);
         *reinterpret_cast<float4 *>(&sQ[qh][d0]) = y;
         const float yy[4] = {y.x, y.y, y.z, y.w};
         s16x4_t hv, lv;
@@ -208,7 +181,7 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
     }
     if (newtok) {
         /* the new token: k_norm + RoPE in fp32, cache row write (bf16) */
-        const float4 y = norm_rope_head(xk, wk, rc, rs, lane);
+        const float4 y = q35_norm_rope_head(xk, wk, rc, rs, lane);
         *reinterpret_cast<float4 *>(&sKn[d0]) = y;
         *reinterpret_cast<float4 *>(&sVn[d0]) = xv;
         if (p.k_post) *reinterpret_cast<float4 *>(p.k_post + (size_t)g * D + d0) = y;

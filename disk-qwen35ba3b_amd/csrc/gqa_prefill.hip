@@ -1,0 +1,324 @@
+/*
+ * gqa_prefill.hip -- causal GQA prefill of B tokens on gfx950: fp16 MFMA
+ * flash attention.
+ *
+ * Replaces the serial gqa_body loop of ds4f_attn_gqa_chunk
+ * (src/attn_qwen.c:1222-1231): the results equal B decode steps in order.
+ *
+ * 1. prep:   one workgroup per new token: q_norm / k_norm + half-split RoPE
+ *            (src/attn_qwen.c:287-326), the bf16 cache rows of k and v, and
+ *            fp16 copies of q, k, v in MFMA-ready workspaces.
+ * 2. prefix: cache rows of positions before t0 (earlier chunks) into the
+ *            fp16 key / value workspaces; zero padding rows (only launched
+ *            when there are such rows).
+ * 3. attn:   grid = (16-position q blocks, kv heads), 4 waves.  A workgroup
+ *            serves the 8 q heads of its kv head (wave w: heads 2w, 2w+1 x
+ *            16 positions = 32 columns), so every K / V tile staged in LDS
+ *            feeds 128 query rows.  Per 32-key block:
+ *              S^T[32 key][32 q] = K Q^T   (16 x v_mfma_f32_32x32x16_f16),
+ *              online softmax per column (rescaled only when a column max
+ *              grows by more than 8, which keeps P <= e^8 in fp16),
+ *              O^T[256][32 q] += V^T P^T  (16 x 32x32x16 f16; the S^T
+ *              accumulator registers are P's B operand as they stand, the
+ *              value tile is stored in the matching key order).
+ *            Output O / l times sigmoid(gate), fp32.
+ * Operands are fp16 (11-bit mantissa): a single MFMA pass keeps the
+ * outputs within the parity bar (max abs error ~1e-3 against the fp32
+ * reference at T = 4096), where bf16 operands would not.
+ */
+#include "q35_device.h"
+#include "q35_launch.h"
+
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
+
+namespace {
+
+constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
+constexpr int KPAD = D + 8;     /* LDS key-row stride (halfs): 528 B */
+constexpr int VPAD = 32 + 8;    /* LDS value-row stride (halfs): 80 B, conflict-free */
+constexpr float SCALE = 0.0625f;
+constexpr float RESCALE_MARGIN = 8.0f;
+
+__device__ __forceinline__ uint16_t f16_bits(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+/* slot of key r (0..31) of a block inside the value tile: within each
+ * 16-key k-step the MFMA B operand of lane half h holds keys
+ * {4h..4h+3, 8+4h..8+4h+3}, so slot order is 0-3, 8-11, 4-7, 12-15 */
+__device__ __forceinline__ int v_slot(int r) {
+    const int ks = r >> 4, r16 = r & 15;
+    const int s16 = (r16 < 8) ? ((r16 >> 2) * 8 + (r16 & 3)) : (((r16 - 8) >> 2) * 8 + 4 + (r16 & 3));
+    return ks * 16 + s16;
+}
+
+__global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
+    const int b = blockIdx.x, pos = p.t0 + b;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63, d0 = lane * 4;
+    const float *rope = p.rope + (size_t)pos * RD;
+
+    float4 xq[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++)
+        xq[hh] = *reinterpret_cast<const float4 *>(p.q_gate + ((size_t)b * p.heads + 4 * w + hh) * 2 * D + d0);
+    const uint2 wq = *reinterpret_cast<const uint2 *>(p.qn_w + d0);
+    float4 rc = make_float4(1.f, 1.f, 1.f, 1.f), rs = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane < RD / 4) {
+        rc = *reinterpret_cast<const float4 *>(rope + (d0 & (RD / 2 - 1)));
+        rs = *reinterpret_cast<const float4 *>(rope + RD / 2 + (d0 & (RD / 2 - 1)));
+    }
+    float4 xk[2], xv[2];
+    uint2 wk = make_uint2(0, 0);
+    if (w == 0) {
+        wk = *reinterpret_cast<const uint2 *>(p.kn_w + d0);
+#pragma unroll
+        for (int g = 0; g < 2; g++)
+            xk[g] = *reinterpret_cast<const float4 *>(p.k_in + ((size_t)b * p.kv_heads + g) * D + d0);
+    }
+    if (w == 1) {
+#pragma unroll
+        for (int g = 0; g < 2; g++)
+            xv[g] = *reinterpret_cast<const float4 *>(p.v_in + ((size_t)b * p.kv_heads + g) * D + d0);
+    }
+
+    const int qb = b >> 4, qp = b & 15;
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) {
+        const int head = 4 * w + hh, g = head / G, hl = head % G;
+        const float4 y = q35_norm_rope_head(xq[hh], wq, rc, rs, lane);
+        uint16_t *dst = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + qp) * D + d0;
+        const uint2 pk = make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
+                                    (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
+        *reinterpret_cast<uint2 *>(dst) = pk;
+    }
+    const int kb = pos >> 5, kr = pos & 31;
+    if (w == 0) {
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const float4 y = q35_norm_rope_head(xk[g], wk, rc, rs, lane);
+            if (p.k_post)
+                *reinterpret_cast<float4 *>(p.k_post + ((size_t)b * p.kv_heads + g) * D + d0) = y;
+            uint16_t *dst = p.kw + (((size_t)g * p.kbt + kb) * 32 + kr) * D + d0;
+            *reinterpret_cast<uint2 *>(dst) =
+                make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
+                           (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
+            const float yy[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) p.kt[q35_k_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(yy[e]);
+        }
+    }
+    if (w == 1) {
+        const int slot = v_slot(kr);
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const float vv[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                p.vw[(((size_t)g * p.kbt + kb) * D + d0 + e) * 32 + slot] = f16_bits(vv[e]);
+                p.vt[q35_v_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(vv[e]);
+            }
+        }
+    }
+}
+
+/* key / value workspace rows that the prep kernel does not write: positions
+ * [0, t0) from the bf16 cache and padding positions [t0+B, 32*kbt) as
+ * zeros.  Threads cover (kv head, row r of n_rows, dim); row r maps to
+ * position r below t0, else to the padding. */
+__global__ void prefix_kernel(Q35GqaPrefill p, int n_rows) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)p.kv_heads * n_rows * D) return;
+    const int g = (int)(i / ((int64_t)n_rows * D));
+    const int r = (int)((i / D) % n_rows), d = (int)(i % D);
+    const int pos = r < p.t0 ? r : p.t0 + p.B + (r - p.t0);
+    float kf = 0.0f, vf = 0.0f;
+    if (pos < p.t0) {
+        kf = q35_bf2f(p.kt[q35_k_index(g, pos, d, p.t_tiles)]);
+        vf = q35_bf2f(p.vt[q35_v_index(g, pos, d, p.t_tiles)]);
+    }
+    const int kb = pos >> 5, kr = pos & 31;
+    p.kw[(((size_t)g * p.kbt + kb) * 32 + kr) * D + d] = f16_bits(kf);
+    p.vw[(((size_t)g * p.kbt + kb) * D + d) * 32 + v_slot(kr)] = f16_bits(vf);
+}
+
+/* q workspace rows [B, 16*nqb) of the last block: zeros */
+__global__ void qpad_kernel(Q35GqaPrefill p, int n_pad) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)p.kv_heads * G * n_pad * D) return;
+    const int d = (int)(i % D);
+    const int64_t row = i / D;
+    const int qpos = p.B + (int)(row % n_pad);
+    const int hl = (int)((row / n_pad) % G), g = (int)(row / ((int64_t)n_pad * G));
+    p.qw[((((size_t)g * p.nqb + (qpos >> 4)) * G + hl) * 16 + (qpos & 15)) * D + d] = 0;
+}
+
+__global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
+    const int g = blockIdx.y;
+    const int qb = p.nqb - 1 - (int)blockIdx.x;          /* longest key range first */
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int h = lane >> 5, col = lane & 31;
+    const int q0 = p.t0 + 16 * qb;
+    const int qpos = q0 + (col & 15);
+    const int hl = 2 * w + (col >> 4);
+    const int end = p.t0 + p.B;
+    const int n_keys = min(q0 + 16, end);
+    const int nkb = (n_keys + 31) >> 5;
+
+    __shared__ _Float16 sK[2][32 * KPAD];
+    __shared__ _Float16 sV[2][D * VPAD];
+
+    /* Q^T as the B operand for the wave's 32 columns, all 16 k-steps */
+    const uint16_t *qrow = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + (col & 15)) * D;
+    f16x8_t qop[16];
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++)
+        qop[ks] = *reinterpret_cast<const f16x8_t *>(qrow + 16 * ks + 8 * h);
+
+    /* staging: thread t copies key row t>>3 (64 B at column chunk t&7) and
+     * value row t (its 32 keys, 64 B) of a block */
+    uint4 stK[4], stV[4];
+    const uint16_t *kwb = p.kw + (size_t)g * p.kbt * 32 * D + (t >> 3) * D + (t & 7) * 32;
+    const uint16_t *vwb = p.vw + (size_t)g * p.kbt * D * 32 + t * 32;
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            stK[u] = *reinterpret_cast<const uint4 *>(kwb + (size_t)kb * 32 * D + u * 8);
+            stV[u] = *reinterpret_cast<const uint4 *>(vwb + (size_t)kb * D * 32 + u * 8);
+        }
+    };
+    auto sstore = [&](int buf) {
+        _Float16 *kd = &sK[buf][(t >> 3) * KPAD + (t & 7) * 32];
+        _Float16 *vd = &sV[buf][t * VPAD];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            *reinterpret_cast<uint4 *>(kd + u * 8) = stK[u];
+            *reinterpret_cast<uint4 *>(vd + u * 8) = stV[u];
+        }
+    };
+
+    f32x16_t acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[dt][i] = 0.0f;
+    float m_used = -INFINITY, l_run = 0.0f;
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; kb++) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) gload(kb + 1);
+        /* S^T = K Q^T: lane holds column col, keys 32kb + 8j + 4h + i' */
+        f32x16_t s;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) {
+            const f16x8_t a = *reinterpret_cast<const f16x8_t *>(&sK[buf][col * KPAD + 16 * ks + 8 * h]);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[ks], s, 0, 0, 0);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int key = 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
+            const float v = (key <= qpos && key < end) ? s[i] * SCALE : -INFINITY;
+            s[i] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool need = mx > m_used + RESCALE_MARGIN;
+        if (__any(need)) {
+            const float m_new = need ? mx : m_used;
+            const float alpha = q35_exp(m_used - m_new);   /* -inf -> 0 on first use */
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) acc[dt] *= alpha;
+            m_used = m_new;
+        }
+        f16x8_t pb[2];
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float pv = q35_exp(s[i] - m_used);
+            ps += pv;
+            pb[i >> 3][i & 7] = (_Float16)pv;
+        }
+        l_run += ps;
+        /* O^T += V^T P^T */
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const f16x8_t a = *reinterpret_cast<const f16x8_t *>(
+                    &sV[buf][(32 * dt + col) * VPAD + 16 * ks + 8 * h]);
+                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[ks], acc[dt], 0, 0, 0);
+            }
+        }
+        if (kb + 1 < nkb) {
+            sstore(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    const float L = l_run + __shfl_xor(l_run, 32);
+    if (qpos < end) {
+        const int b = qpos - p.t0, head = g * G + hl;
+        const float *gate = p.q_gate + ((size_t)b * p.heads + head) * 2 * D + D;
+        float *out = p.attn_out + ((size_t)b * p.heads + head) * D;
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 32 * dt + 8 * j + 4 * h;
+                const float4 gv = *reinterpret_cast<const float4 *>(gate + d);
+                float4 o;
+                o.x = acc[dt][4 * j + 0] * inv * q35_sigmoid(gv.x);
+                o.y = acc[dt][4 * j + 1] * inv * q35_sigmoid(gv.y);
+                o.z = acc[dt][4 * j + 2] * inv * q35_sigmoid(gv.z);
+                o.w = acc[dt][4 * j + 3] * inv * q35_sigmoid(gv.w);
+                *reinterpret_cast<float4 *>(out + d) = o;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *qw, size_t *kw,
+                                         size_t *vw) {
+    const size_t nqb = (size_t)(B + 15) / 16, kbt = (size_t)(t0 + B + 31) / 32;
+    *qw = (size_t)kv_heads * nqb * G * 16 * D * 2;
+    *kw = (size_t)kv_heads * kbt * 32 * D * 2;
+    *vw = *kw;
+}
+
+extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stream) {
+    Q35GqaPrefill p = *pin;
+    if (p.heads != p.kv_heads * G || p.kv_heads != 2 || p.B < 1 || p.t0 < 0) return hipErrorInvalidValue;
+    p.nqb = (p.B + 15) / 16;
+    p.kbt = (p.t0 + p.B + 31) / 32;
+    hipLaunchKernelGGL(prep_kernel, dim3(p.B), dim3(256), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int n_rows = p.t0 + (p.kbt * 32 - (p.t0 + p.B));    /* prefix + key padding */
+    if (n_rows > 0) {
+        const int64_t n = (int64_t)p.kv_heads * n_rows * D;
+        hipLaunchKernelGGL(prefix_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
+                           n_rows);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const int n_pad = p.nqb * 16 - p.B;
+    if (n_pad > 0) {
+        const int64_t n = (int64_t)p.kv_heads * G * n_pad * D;
+        hipLaunchKernelGGL(qpad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
+                           n_pad);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(attn_kernel, dim3(p.nqb, p.kv_heads), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}

@@ -119,6 +119,34 @@ __device__ __forceinline__ double q35_normal(uint64_t seed, uint64_t tid, uint64
     return sqrt(-2.0 * log(1.0 - u1)) * cos(2.0 * 3.141592653589793 * u2);
 }
 
+/* GQA head prologue: RMSNorm (double sum of squares, eps on the mean, x / r * w) and
+ * half-split RoPE of one head held as 4 dims per lane (dims 4l..4l+3).
+ * w: the 4 bf16 weights of those dims; c, s: cos / sin of rotary index
+ * (4l & 31) .. +3, used by lanes < 16 only. */
+__device__ __forceinline__ float4 q35_norm_rope_head(float4 x, uint2 w, float4 c, float4 s,
+                                                     int lane) {
+#pragma clang fp contract(off)
+    double ss = (double)x.x * x.x + (double)x.y * x.y + (double)x.z * x.z + (double)x.w * x.w;
+    ss = q35_wave_sum(ss);
+    const float r = sqrtf((float)(ss / (double)Q35_GQA_D) + 1e-6f);
+    float v[4] = {x.x, x.y, x.z, x.w};
+    const uint16_t wt[4] = {(uint16_t)(w.x & 0xffff), (uint16_t)(w.x >> 16),
+                            (uint16_t)(w.y & 0xffff), (uint16_t)(w.y >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = v[e] / r * q35_bf2f(wt[e]);
+    /* RoPE pairs (i, i+32), i < 32: lanes 0..7 hold i, lanes 8..15 hold i+32 */
+    const float cc[4] = {c.x, c.y, c.z, c.w}, sn[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float pr = q35_xor8(v[e]);
+        if (lane < Q35_ROPE_DIMS / 8)
+            v[e] = v[e] * cc[e] - pr * sn[e];        /* x0*c - x1*s */
+        else if (lane < Q35_ROPE_DIMS / 4)
+            v[e] = pr * sn[e] + v[e] * cc[e];        /* x0*s + x1*c */
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 /* Device K / V tile addressing (see q35_launch.h). */
 __device__ __forceinline__ size_t q35_k_index(int kvh, int p, int d, int t_tiles) {
     return ((((size_t)kvh * t_tiles + (p >> 4)) * (Q35_GQA_D / 32) + (d >> 5)) * 16 + (p & 15)) * 32 +

@@ -64,8 +64,10 @@ __global__ void synth_kernel(void *dst, int64_t n, int dtype, int dist, double p
     const float f = (float)v;
     if (dtype == 0)
         static_cast<float *>(dst)[i] = f;
-    else
+    else if (dtype == 1)
         static_cast<uint16_t *>(dst)[i] = q35_f2bf(f);
+    else
+        static_cast<float *>(dst)[i] = q35_bf2f(q35_f2bf(f));
 }
 
 /* element i of the logical [pos][kvh][dim] order -> tiles */

@@ -43,6 +43,7 @@ _SIGS = {
     "ds4f_gpu_gqa_prefill": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "ds4f_gpu_lin_prefill": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "ds4f_hip_gqa_decode_async": ([_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "ds4f_hip_gqa_prefill_async": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "ds4f_hip_lin_decode_async": ([_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp], _i),
     "ds4f_hip_synth": ([_vp, _i64, _i, _i, _d, _d, _u64, _u64, _vp], _i),
@@ -69,6 +70,13 @@ def load():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"HIP attention plugin not built: {LIB_PATH} is missing "
                                "(run __graft_entry__.build())")
+        # torch's wheel ships its own HIP runtime under the same soname
+        # (libamdhip64.so.7).  Importing torch first makes the plugin bind to
+        # that copy, so the process holds ONE runtime and torch tensors,
+        # streams and the plugin's kernels share it; loading the plugin first
+        # would pull in /opt/rocm's copy beside torch's and the second
+        # runtime to initialise finds no devices.
+        import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         for name, (args, res) in _SIGS.items():
             fn = getattr(L, name)

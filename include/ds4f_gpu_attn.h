@@ -109,9 +109,9 @@ int ds4f_gpu_lin_decode(int L, int token, float *qkv, const float *z,
                         const uint16_t *dt_bias, const uint16_t *norm_w,
                         float *out);
 
-/* Prefill of B tokens t0..t0+B-1 of a GQA layer: the same results as B
- * ds4f_gpu_gqa_decode calls in order.  Arrays are [B][...] of the decode
- * shapes. */
+/* Prefill of B tokens t0..t0+B-1 of a GQA layer: the results of B
+ * ds4f_gpu_gqa_decode calls in order, computed as one causal flash
+ * attention (fp16 MFMA).  Arrays are [B][...] of the decode shapes. */
 int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k,
                          const float *v, const uint16_t *qn_w,
                          const uint16_t *kn_w, float *attn_out);
@@ -133,6 +133,12 @@ int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate,
                               const float *k, const float *v,
                               const uint16_t *qn_w, const uint16_t *kn_w,
                               float *attn_out, float *k_post, void *stream);
+/* Prefill of B tokens t0.. of a GQA layer (fp16 MFMA flash attention).
+ * Allocates its workspace on first use or growth (not capturable then). */
+int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate,
+                               const float *k, const float *v,
+                               const uint16_t *qn_w, const uint16_t *kn_w,
+                               float *attn_out, float *k_post, void *stream);
 int ds4f_hip_lin_decode_async(int L, int token, const float *qkv,
                               const float *z, const float *a, const float *b,
                               const uint16_t *conv_w, const float *A_log,
@@ -142,7 +148,8 @@ int ds4f_hip_lin_decode_async(int L, int token, const float *qkv,
 /* ---- synthetic state for benchmarks and tests ------------------------- *
  * Fill device memory with the splitmix64 / Box-Muller streams of the
  * workload generator (seed, tensor id; index = logical element index).
- * dtype 0 = float32, 1 = bf16; dist 0 = normal(p0 = mean, p1 = sigma),
+ * dtype 0 = float32, 1 = bf16, 2 = float32 holding the bf16-rounded value;
+ * dist 0 = normal(p0 = mean, p1 = sigma),
  * 1 = uniform(p0 = lo, p1 = hi). */
 int ds4f_hip_synth(void *dst, int64_t n, int dtype, int dist, double p0,
                    double p1, uint64_t seed, uint64_t tid, void *stream);

@@ -46,6 +46,8 @@ def lib():
         L.orc_lin_prefill.argtypes = [i, i, i, i, i, i, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                       _u16p, _f32p, _u16p, _u16p, _f32p]
         L.orc_lin_prefill.restype = i
+        L.orc_gqa_cache_row.argtypes = [i, i, i, _f32p, _f32p, _u16p, _f32p]
+        L.orc_gqa_cache_row.restype = None
         L.orc_rope_table.argtypes = [i, i, ctypes.c_double, _f32p, _f32p]
         L.orc_rope_table.restype = None
         L.orc_rmsnorm.argtypes = [_u16p, i, _f32p]
@@ -113,6 +115,22 @@ def lin_prefill(conv_ring, S, t0, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w,
     if rc != 0:
         raise RuntimeError("orc_lin_prefill failed")
     return out, qkv
+
+
+def gqa_cache_rows(k, v, kn_w, t0, kv_heads, head_dim):
+    """fp32 cache rows of tokens t0.. (k normed + rotated, v raw), [B][2*kvh*d]."""
+    B = k.shape[0]
+    rows = np.zeros((B, 2 * kv_heads * head_dim), np.float32)
+    kk = _c(k, np.float32).reshape(B, -1).copy()
+    vv = _c(v, np.float32).reshape(B, -1)
+    knw = _c(kn_w, np.uint16)
+    for b in range(B):
+        kb = kk[b].copy()
+        out = np.zeros(2 * kv_heads * head_dim, np.float32)
+        lib().orc_gqa_cache_row(kv_heads, head_dim, t0 + b, kb, np.ascontiguousarray(vv[b]), knw,
+                                out)
+        rows[b] = out
+    return rows
 
 
 def rope_table(token, rd=64, theta=1e7):

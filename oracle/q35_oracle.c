@@ -233,6 +233,18 @@ int orc_lin_body(int k_heads, int v_heads, int kd, int vd, int token,
     return 0;
 }
 
+void orc_gqa_cache_row(int kv_heads, int kh, int token, float *k, const float *v,
+                       const uint16_t *kn_w, float *row_out) {
+    int rd = (int)(kh * 0.25f);
+    float cs[128];
+    float *cos_t = cs, *sin_t = cs + 64;
+    for (int g = 0; g < kv_heads; g++) orc_rmsnorm(kn_w, kh, k + (size_t)g * kh);
+    orc_rope_table(token, rd, ROPE_THETA, cos_t, sin_t);
+    for (int g = 0; g < kv_heads; g++) rope_rotate(k + (size_t)g * kh, rd, cos_t, sin_t);
+    memcpy(row_out, k, (size_t)kv_heads * kh * sizeof(float));
+    memcpy(row_out + (size_t)kv_heads * kh, v, (size_t)kv_heads * kh * sizeof(float));
+}
+
 int orc_gqa_prefill(int heads, int kv_heads, int kh, int max_tokens,
                     float *kv_layer, int t0, int B, const float *q, float *k,
                     const float *v, const uint16_t *qn_w,

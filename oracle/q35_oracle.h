@@ -65,6 +65,13 @@ int orc_lin_body(int k_heads, int v_heads, int kd, int vd, int token,
                  const float *A_log, const uint16_t *dt_bias,
                  const uint16_t *norm_w, float *out);
 
+/* The cache row gqa_body writes for `token` without the attention: k normed
+ * (k_norm) and rotated in place (src/attn_qwen.c:292-293, :297-325), then
+ * [k | v] copied to row_out [2*kv_heads*kh].  Lets a test build a long
+ * cache cheaply and run orc_gqa_body only at sampled tokens. */
+void orc_gqa_cache_row(int kv_heads, int kh, int token, float *k, const float *v,
+                       const uint16_t *kn_w, float *row_out);
+
 /* Serial prefill: orc_gqa_body for t = t0 .. t0+B-1 in order
  * (src/attn_qwen.c:1222-1231).  q: [B][heads*2*kh], k (in place), v:
  * [B][kv_heads*kh], attn_out: [B][heads*kh]. */

@@ -1,0 +1,120 @@
+"""GPU parity of the prefill kernels against the oracle (needs an MI355X).
+
+GQA prefill runs fp16 MFMA flash attention; the bar is max |gpu - oracle|
+<= 2e-3 on the attention outputs.  At T = 4096 the oracle's O(T^2) serial
+loop is replaced by its cache-row helper (cheap) plus the oracle body at
+sampled tokens, which is the same computation at those tokens.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from ds4f_hip import synth as S
+from ds4f_hip import workloads as W
+from ds4f_hip.attn import GpuAttention, KvCache
+
+pytestmark = pytest.mark.gpu
+
+GQ = W.GqaGeom()
+ATOL = 2e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _err(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    mx = float(np.abs(got - ref).max())
+    rr = float(np.sqrt(((got - ref) ** 2).sum() / max((ref ** 2).sum(), 1e-300)))
+    return mx, rr
+
+
+def _sampled_reference(q, k, v, qn, kn, t0, past_rows, samples):
+    """Oracle outputs at sampled tokens of a prefill starting at t0 whose
+    cache holds past_rows [t0][1024] (fp32)."""
+    B = q.shape[0]
+    rows = O.gqa_cache_rows(k, v, kn, t0, GQ.kv_heads, GQ.head_dim)
+    kv = np.zeros((t0 + B, 2 * GQ.kv_heads * GQ.head_dim), np.float32)
+    if t0:
+        kv[:t0] = past_rows
+    kv[t0:] = rows
+    out = {}
+    for b in samples:
+        # the body rewrites row t0+b with the values the helper put there
+        o, _ = O.gqa_body(kv, t0 + b, q[b].reshape(-1), k[b].reshape(-1), v[b].reshape(-1), qn,
+                          kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+        out[b] = o
+    return out, rows
+
+
+@pytest.mark.parametrize("T", [1, 17, 64, 200])
+def test_gqa_prefill_small_full_check(T):
+    qn, kn = W.gqa_weights(GQ)
+    q, k, v = W.gqa_prefill_tokens(GQ, T)
+    cache = KvCache(1, T + 16)
+    ref_kv = cache.kv[0].copy()
+    ga = GpuAttention([2], T + 16, cache)
+    out, kp = ga.gqa_prefill(0, 0, q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1), qn, kn)
+    ref, rk = O.gqa_prefill(ref_kv, 0, q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1), qn,
+                            kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+    mx, rr = _err(out, ref)
+    _say(f"gqa prefill T={T}: max abs {mx:.3e} rel-rms {rr:.3e}")
+    assert mx <= ATOL
+    assert _err(kp, rk)[0] < 1e-5
+    ga.sync(0, to_host=True, n_kv_tokens=T)
+    half = GQ.kv_heads * GQ.head_dim
+    assert np.array_equal(cache.kv[0, :T, :half], S.bf16_round(rk))
+    assert np.array_equal(cache.kv[0, :T, half:], S.bf16_round(v.reshape(T, -1)))
+    ga.close()
+
+
+def test_gqa_prefill_4096_sampled():
+    T = 4096
+    _say("gqa prefill T=4096")
+    qn, kn = W.gqa_weights(GQ)
+    q, k, v = W.gqa_prefill_tokens(GQ, T)
+    ga = GpuAttention([2], T + 64, None)
+    out, kp = ga.gqa_prefill(0, 0, q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1), qn, kn)
+    rng = np.random.default_rng(7)
+    samples = sorted(set([0, 1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 100, 1023, 2047, 4095] +
+                         list(rng.integers(0, T, 12))))
+    refs, rows = _sampled_reference(q, k, v, qn, kn, 0, None, samples)
+    worst = 0.0
+    for b in samples:
+        worst = max(worst, _err(out[b], refs[b])[0])
+    _say(f"  sampled tokens {len(samples)}: worst max abs {worst:.3e}")
+    assert worst <= ATOL
+    half = GQ.kv_heads * GQ.head_dim
+    assert np.abs(kp - rows[:, :half]).max() < 1e-5
+    ga.close()
+
+
+def test_gqa_prefill_continues_a_cache():
+    """Chunked prefill: 100 tokens, then 77 more at t0 = 100 (unaligned),
+    then one decode step; all against the oracle's serial body."""
+    qn, kn = W.gqa_weights(GQ)
+    q, k, v = W.gqa_prefill_tokens(GQ, 178)
+    cache = KvCache(1, 256)
+    ref_kv = cache.kv[0].copy()
+    ga = GpuAttention([2], 256, cache)
+    worst = 0.0
+    for t0, B in ((0, 100), (100, 77)):
+        sl = slice(t0, t0 + B)
+        out, _ = ga.gqa_prefill(0, t0, q[sl].reshape(B, -1), k[sl].reshape(B, -1),
+                                v[sl].reshape(B, -1), qn, kn)
+        ref, _ = O.gqa_prefill(ref_kv, t0, q[sl].reshape(B, -1), k[sl].reshape(B, -1),
+                               v[sl].reshape(B, -1), qn, kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+        # the device cache holds bf16 rows: give the oracle the same rows
+        ref_kv[sl] = S.bf16_round(ref_kv[sl])
+        worst = max(worst, _err(out, ref)[0])
+    out, _ = ga.gqa_decode(0, 177, q[177], k[177], v[177], qn, kn)
+    ref, _ = O.gqa_body(ref_kv, 177, q[177].reshape(-1), k[177].reshape(-1), v[177].reshape(-1),
+                        qn, kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+    worst = max(worst, _err(out, ref)[0])
+    _say(f"chunked prefill + decode: worst max abs {worst:.3e}")
+    assert worst <= ATOL
+    ga.close()
