@@ -611,3 +611,18 @@ int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid, v
     HIPCHK(q35_synth_conv(layer_conv(P.slot[L]), P.rows, token, seed, tid, pick(stream)));
     return 0;
 }
+
+/* ---- output-head matvecs: not part of this plugin (gpu_stub.c semantics) */
+int ds4f_gpu_mlx4_matvec(const uint32_t *vals, const uint16_t *scales, const uint16_t *biases,
+                         int R, int C, const float *x, float *y) {
+    (void)vals; (void)scales; (void)biases; (void)R; (void)C; (void)x; (void)y;
+    return -1;
+}
+
+int ds4f_gpu_mlx4_batch(const uint32_t *const *vals, const uint16_t *const *scales,
+                        const uint16_t *const *biases, const float *const *xs, float *const *ys,
+                        const void *const *ids, int R, int C, int njobs) {
+    (void)vals; (void)scales; (void)biases; (void)xs; (void)ys; (void)ids;
+    (void)R; (void)C; (void)njobs;
+    return -1;
+}

@@ -51,6 +51,8 @@ _SIGS = {
     "ds4f_hip_synth_lin_state": ([_i, _d, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_conv_history": ([_i, _i, _u64, _u64, _vp], _i),
     "ds4f_gpu_last_error": ([], ctypes.c_char_p),
+    "ds4f_gpu_mlx4_matvec": ([_vp, _vp, _vp, _i, _i, _vp, _vp], _i),
+    "ds4f_gpu_mlx4_batch": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i], _i),
 }
 
 _lib = None

@@ -164,6 +164,20 @@ int ds4f_hip_synth_lin_state(int L, double sigma, uint64_t seed, uint64_t tid,
 int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid,
                                 void *stream);
 
+/* ---- the rest of include/ds4f/gpu.h (:29-54) -------------------------- *
+ * The output-head MLX-4bit matvecs are outside this plugin: they return -1
+ * (unavailable), exactly as src/gpu_stub.c does, so the engine keeps its
+ * CPU matvec.  They are exported so this library can stand in for
+ * gpu_stub.c in the engine's GPU_SRC slot. */
+int ds4f_gpu_mlx4_matvec(const uint32_t *vals, const uint16_t *scales,
+                         const uint16_t *biases, int R, int C,
+                         const float *x, float *y);
+int ds4f_gpu_mlx4_batch(const uint32_t *const *vals,
+                        const uint16_t *const *scales,
+                        const uint16_t *const *biases,
+                        const float *const *xs, float *const *ys,
+                        const void *const *ids, int R, int C, int njobs);
+
 /* Last error text of the plugin (static storage). */
 const char *ds4f_gpu_last_error(void);
 
