@@ -20,6 +20,10 @@ host, one thread, on a bounded sample of the same steps).
 Other workloads (one JSON line each, same fields):
   gqa_prefill   causal GQA prefill of --tokens (4096) tokens, one layer,
                 bf16-valued q|gate/k/v N(0,1); MFMA roofline.
+  lin_prefill   gated delta-rule prefill of --tokens (4096) tokens, one
+                layer, zero state and conv ring, fp32 qkv/z/a/b N(0,1);
+                chunked form on fp32 MFMA, roofline against the fp32 MFMA
+                peak.
 """
 from __future__ import annotations
 
@@ -35,6 +39,7 @@ sys.path.insert(0, os.path.join(ROOT, "disk-qwen35ba3b_amd"))
 
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0     # dense bf16 / fp16
+MFMA_F32_PEAK_TFLOPS = 157.3  # dense fp32
 METRIC = "GQA+delta-rule attn tokens/s and HBM GB/s %peak, decode @32K ctx, 1 GPU"
 
 
@@ -64,7 +69,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU-baseline sample budget (whole steps, at least one)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill"])
+    ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill",
+                                                                    "lin_prefill"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     args = ap.parse_args()
 
@@ -74,6 +80,8 @@ def main() -> int:
         return 2
     if args.workload == "gqa_prefill":
         return run_gqa_prefill(args)
+    if args.workload == "lin_prefill":
+        return run_lin_prefill(args)
     return run_stack_decode(args)
 
 
@@ -374,6 +382,117 @@ def run_gqa_prefill(args) -> int:
             "scaling": "weak", "vs_baseline": None, "dtype": "fp16-mfma/fp32",
             "data": "synthetic (splitmix64 streams, seed 0: bf16-valued q|gate, k, v N(0,1))",
             "config": {"workload": "gqa causal prefill", "tokens": T, "t0": 0, "layers": 1},
+            "wall_ms_per_step": round(sec / K * 1e3, 4),
+            "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def lin_prefill_flops(T: int, C: int = 64, heads: int = 32, dk: int = 128, dv: int = 128) -> float:
+    """Algorithmic flops of the chunked delta-rule prefill: per (value head,
+    chunk) 2C^2(3dk + 2dv) (K K^T, Q K^T, W, U, Pm Delta) + 6 C dk dv (W S,
+    Q S, Kd^T Delta) + 2C^3/3 (the triangular solve)."""
+    per = 2.0 * C * C * (3 * dk + 2 * dv) + 6.0 * C * dk * dv + 2.0 * C ** 3 / 3
+    return per * heads * ((T + C - 1) // C)
+
+
+def run_lin_prefill(args) -> int:
+    """One delta-rule prefill of T tokens (one layer, t0 = 0, zero state and
+    conv ring) per step."""
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip import synth as S
+    from ds4f_hip import workloads as W
+    from ds4f_hip.attn import GpuAttention, dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    lg = W.LinGeom()
+    T, K, WU, seed = args.tokens, max(1, min(args.steps, 50)), max(1, min(args.warmup, 5)), args.seed
+    ga = GpuAttention([1], T + 64, None)       # zero state, zero ring
+    nz = lg.v_heads * lg.vd
+    qkv = torch.empty((T, lg.rows), dtype=torch.float32, device=dev)
+    z = torch.empty((T, nz), dtype=torch.float32, device=dev)
+    a = torch.empty((T, lg.v_heads), dtype=torch.float32, device=dev)
+    b = torch.empty((T, lg.v_heads), dtype=torch.float32, device=dev)
+    for t in range(T):     # the per-token streams of workloads.lin_token
+        for buf, n, tid in ((qkv, lg.rows, S.LIN_QKV), (z, nz, S.LIN_Z), (a, lg.v_heads, S.LIN_A),
+                            (b, lg.v_heads, S.LIN_B)):
+            L.check(lib.ds4f_hip_synth(dptr(buf[t]), n, 0, 0, 0.0, 1.0, seed, S.tid(tid, 0, t),
+                                       None), "synth")
+    wt = W.lin_weights(lg, seed, 0)
+    cw = torch.from_numpy(wt.conv_w.view("int16").reshape(-1).copy()).to(dev)
+    al = torch.from_numpy(wt.A_log.copy()).to(dev)
+    dtb = torch.from_numpy(wt.dt_bias.view("int16").copy()).to(dev)
+    nw = torch.from_numpy(wt.norm_w.view("int16").copy()).to(dev)
+    out = torch.empty((T, nz), dtype=torch.float32, device=dev)
+    post = torch.empty((T, lg.rows), dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    st = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        # every step starts from the zero state (2 MiB fill, inside the timing)
+        L.check(lib.ds4f_hip_synth_lin_state(0, 0.0, seed, S.tid(S.LIN_STATE, 0), st), "reset")
+        L.check(lib.ds4f_hip_lin_prefill_async(0, 0, T, dptr(qkv), dptr(z), dptr(a), dptr(b),
+                                               dptr(cw), dptr(al), dptr(dtb), dptr(nw),
+                                               dptr(out), dptr(post), st), "lin prefill")
+
+    for _ in range(WU):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(K):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    op_us = ev0.elapsed_time(ev1) * 1e3 / K
+    flops = lin_prefill_flops(T)
+    tflops = flops / (op_us * 1e-6) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4),
+                "traffic": None,
+                "kernel": "delta prefill = conv + ring + chunk + scan + gnorm kernels "
+                          "(fp32 MFMA), state reset included",
+                "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the reference prefill is T serial lin_body calls; its cost per
+        # token does not depend on the position: time a prefix of the same
+        # prefill, whole 64-token batches, within the sample budget
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import numpy as np
+        import oracle as O
+        hq, hz, ha, hb = W.lin_tokens(lg, min(T, 4096), seed, 0)
+        ring = np.zeros((4, lg.rows), np.float32)
+        Sh = np.zeros((lg.v_heads, lg.kd, lg.vd), np.float32)
+        done, secs = 0, 0.0
+        while done < hq.shape[0] and (done == 0 or secs < args.cpu_seconds):
+            n = min(64, hq.shape[0] - done)
+            sl = slice(done, done + n)
+            c0 = time.perf_counter()
+            O.lin_prefill(ring, Sh, done, hq[sl], hz[sl], ha[sl], hb[sl], wt.conv_w, wt.A_log,
+                          wt.dt_bias, wt.norm_w, lg.k_heads, lg.v_heads, lg.kd, lg.vd)
+            secs += time.perf_counter() - c0
+            done += n
+        cpu = {"value": round(done / secs, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"oracle serial lin_body over the first {done} tokens of the same "
+                         f"prefill ({secs:.1f} s; per-token cost is position-independent)"}
+    ga.close()
+    line = {"metric": f"gated delta-rule prefill tokens/s ({T} tokens, 32 heads 128x128, 1 layer)",
+            "value": round(T / (op_us * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+            "warmup": WU, "ms_per_step": round(op_us / 1e3, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (splitmix64 streams, seed 0: qkv, z, a, b N(0,1) per token; "
+                    "zero state and conv ring)",
+            "config": {"workload": "delta-rule prefill", "tokens": T, "t0": 0, "chunk": 64,
+                       "layers": 1},
             "wall_ms_per_step": round(sec / K * 1e3, 4),
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)

@@ -455,6 +455,58 @@ int ds4f_hip_lin_decode_async(int L, int token, const float *qkv, const float *z
     return 0;
 }
 
+int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const float *z,
+                               const float *a, const float *b, const uint16_t *conv_w,
+                               const float *A_log, const uint16_t *dt_bias,
+                               const uint16_t *norm_w, float *out, float *qkv_post,
+                               void *stream) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;   /* src/attn_qwen.c:882 */
+    if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
+    size_t bytes;
+    q35_lin_prefill_ws_bytes(B, P.g.n_heads, P.vh, qkv_post == NULL, &bytes);
+    if (ensure_ws(bytes) != 0) return -1;
+    Q35LinPrefill p;
+    memset(&p, 0, sizeof p);
+    p.qkv = qkv;
+    p.z = z;
+    p.a = a;
+    p.b = b;
+    p.conv_w = conv_w;
+    p.A_log = A_log;
+    p.dt_bias = dt_bias;
+    p.norm_w = norm_w;
+    p.ring = layer_conv(P.slot[L]);
+    p.state = layer_lin(P.slot[L]);
+    p.out = out;
+    p.t0 = t0;
+    p.B = B;
+    p.n_chunks = (B + 63) / 64;
+    p.k_heads = P.g.n_heads;
+    p.v_heads = P.vh;
+    /* carve the workspace, each piece 256-byte aligned */
+    const size_t nc = (size_t)p.n_chunks, vh = (size_t)P.vh;
+    char *w = (char *)P.d_ws;
+#define CARVE(dst, nfloats)                                   \
+    do {                                                      \
+        (dst) = (float *)w;                                   \
+        w += (((size_t)(nfloats) * sizeof(float)) + 255) & ~(size_t)255; \
+    } while (0)
+    if (qkv_post)
+        p.post = qkv_post;
+    else
+        CARVE(p.post, (size_t)B * P.rows);
+    CARVE(p.gates, (size_t)B * vh * 2);
+    CARVE(p.W, nc * vh * 64 * P.kd);
+    CARVE(p.U, nc * vh * 64 * P.vd);
+    CARVE(p.Pm, nc * vh * 64 * 64);
+    CARVE(p.KdT, nc * vh * P.kd * 64);
+    CARVE(p.gvec, nc * vh * Q35_LIN_GVEC);
+#undef CARVE
+    HIPCHK(q35_lin_prefill(&p, pick(stream)));
+    return 0;
+}
+
 /* ---- host-pointer entry points ----------------------------------------- */
 
 /* Pack host arrays into the pinned stage, one H2D copy; returns device
@@ -571,13 +623,30 @@ int ds4f_gpu_lin_prefill(int L, int t0, int B, float *qkv, const float *z, const
                          const float *b, const uint16_t *conv_w, const float *A_log,
                          const uint16_t *dt_bias, const uint16_t *norm_w, float *out) {
     if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;
+    if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;   /* later tokens: silent skip */
+    if (forced_failure()) return fail_over(t0);
     const int rows = P.rows, VH = P.vh, VD = P.vd;
-    for (int t = 0; t < B; t++) {
-        int rc = ds4f_gpu_lin_decode(L, t0 + t, qkv + (size_t)t * rows, z + (size_t)t * VH * VD,
-                                     a + (size_t)t * VH, b + (size_t)t * VH, conv_w, A_log,
-                                     dt_bias, norm_w, out + (size_t)t * VH * VD);
-        if (rc != 0) return rc;
-    }
+    void *dqkv, *dz, *da, *db, *dcw, *dal, *ddt, *dnw, *dout;
+    Piece pc[8] = {{qkv, (size_t)B * rows * 4, &dqkv},
+                   {z, (size_t)B * VH * VD * 4, &dz},
+                   {a, (size_t)B * VH * 4, &da},
+                   {b, (size_t)B * VH * 4, &db},
+                   {conv_w, (size_t)rows * 4 * 2, &dcw},
+                   {A_log, (size_t)VH * 4, &dal},
+                   {dt_bias, (size_t)VH * 2, &ddt},
+                   {norm_w, (size_t)VD * 2, &dnw}};
+    const size_t ob = (size_t)B * VH * VD * 4, pb = (size_t)B * rows * 4;
+    if (upload(pc, 8, ob + pb, &dout) != 0) return fail_over(t0);
+    float *d_out = (float *)dout, *d_post = (float *)((char *)dout + ob);
+    if (ds4f_hip_lin_prefill_async(L, t0, B, (const float *)dqkv, (const float *)dz,
+                                   (const float *)da, (const float *)db, (const uint16_t *)dcw,
+                                   (const float *)dal, (const uint16_t *)ddt,
+                                   (const uint16_t *)dnw, d_out, d_post, NULL) != 0 ||
+        download(dout, ob + pb) != 0)
+        return fail_over(t0 + B);
+    memcpy(out, P.h_stage, ob);
+    memcpy(qkv, (char *)P.h_stage + ob, pb);
     return 0;
 }
 

@@ -25,20 +25,6 @@ namespace {
 
 constexpr int KD = 128, VD = 128, NT = 1024;
 
-/* Causal conv tap sum + SiLU of one channel (src/attn_qwen.c:493-504): tap k
- * reads position token-3+k (k = 3 is the incoming raw value, x[3]); taps
- * before position 0 are skipped. */
-__device__ __forceinline__ float conv_silu(const float (&x)[4], uint2 wv, int token) {
-#pragma clang fp contract(off)
-    const uint16_t wt[4] = {(uint16_t)(wv.x & 0xffff), (uint16_t)(wv.x >> 16),
-                            (uint16_t)(wv.y & 0xffff), (uint16_t)(wv.y >> 16)};
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-        if (token - 3 + k >= 0) acc += x[k] * q35_bf2f(wt[k]);
-    return acc * q35_sigmoid(acc);
-}
-
 __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     const int h = blockIdx.x;      /* value head */
     const int kh = h >> 1;         /* its key head (src/attn_qwen.c:658) */
@@ -96,7 +82,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     /* ---- prologue: conv + SiLU, ring update, q/k norms, gates ---- */
     float x = 0.0f;
     if (ch >= 0) {
-        x = conv_silu(xin, wv, tok);
+        x = q35_conv_silu(xin, wv, tok);
         /* ring slot token%4 takes the raw row; q/k channels are shared by
          * the two value heads of a key head, the even one writes them */
         if (kind == 2 || (h & 1) == 0) p.ring[(size_t)(tok & 3) * rows + ch] = xin[3];
@@ -105,13 +91,10 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     ss = q35_wave_sum(ss);
     if ((t & 63) == 0 && t < 2 * KD) sred[t >> 6] = ss;
     if (t == 2 * KD + VD) {
-        /* gates (src/attn_qwen.c:545-551, :664-665) */
-#pragma clang fp contract(off)
-        float xa = ga + q35_bf2f(gdt);
-        float sp_ = xa > 0 ? xa + log1pf(expf(-xa)) : log1pf(expf(xa));
-        float g = -expf(gal) * sp_;
+        float g, beta;
+        q35_lin_gates(ga, gb, gal, gdt, &g, &beta);
         sgate[0] = expf(g);
-        sgate[1] = q35_sigmoid(gb);
+        sgate[1] = beta;
     }
     __syncthreads();
     if (kind == 0 || kind == 1) {

@@ -147,6 +147,33 @@ __device__ __forceinline__ float4 q35_norm_rope_head(float4 x, uint2 w, float4 c
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
+/* Causal conv tap sum + SiLU of one delta-rule channel
+ * (src/attn_qwen.c:493-504): tap k reads position pos-3+k (k = 3 is the
+ * incoming raw value); taps before position 0 are skipped.  w holds the
+ * channel's 4 bf16 taps, oldest first. */
+__device__ __forceinline__ float q35_conv_silu(const float (&x)[4], uint2 w, int pos) {
+#pragma clang fp contract(off)
+    const uint16_t wt[4] = {(uint16_t)(w.x & 0xffff), (uint16_t)(w.x >> 16),
+                            (uint16_t)(w.y & 0xffff), (uint16_t)(w.y >> 16)};
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (pos - 3 + k >= 0) acc += x[k] * q35_bf2f(wt[k]);
+    return acc * q35_sigmoid(acc);
+}
+
+/* Delta-rule gates of one value head (src/attn_qwen.c:545-551, :664-665):
+ * log-decay g = -exp(A_log) * softplus(a + dt_bias) in the reference's
+ * branch form, and beta = sigmoid(b). */
+__device__ __forceinline__ void q35_lin_gates(float a, float b, float A_log, uint16_t dt_bias,
+                                              float *g, float *beta) {
+#pragma clang fp contract(off)
+    const float x = a + q35_bf2f(dt_bias);
+    const float sp = x > 0 ? x + log1pf(expf(-x)) : log1pf(expf(x));
+    *g = -expf(A_log) * sp;
+    *beta = q35_sigmoid(b);
+}
+
 /* Device K / V tile addressing (see q35_launch.h). */
 __device__ __forceinline__ size_t q35_k_index(int kvh, int p, int d, int t_tiles) {
     return ((((size_t)kvh * t_tiles + (p >> 4)) * (Q35_GQA_D / 32) + (d >> 5)) * 16 + (p & 15)) * 32 +

@@ -38,6 +38,28 @@ typedef struct Q35LinDecode {
 } Q35LinDecode;
 hipError_t q35_lin_decode(const Q35LinDecode *p, hipStream_t stream);
 
+/* ---- gated delta-rule prefill, chunked (chunk 64, kd = vd = 128) ---- *
+ * Workspaces (fp32), nc = ceil(B/64), VH value heads:
+ *   post  [B][rows]          post-conv, normed q | k | v (the caller's
+ *                            qkv_post, or a workspace)
+ *   gates [B][VH][2]         (log-decay g, beta)
+ *   W, U  [nc][VH][64][128]  Pm [nc][VH][64][64]  KdT [nc][VH][128][64]
+ *   gvec  [nc][VH][Q35_LIN_GVEC]  exp(G_t), exp(G_C - G_t), exp(G_C) */
+#define Q35_LIN_GVEC 256
+typedef struct Q35LinPrefill {
+    const float *qkv, *z, *a, *b;  /* [B][rows], [B][VH*VD], [B][VH], [B][VH] */
+    const uint16_t *conv_w, *dt_bias, *norm_w;
+    const float *A_log;
+    float *ring;                   /* [4][rows] */
+    float *state;                  /* [vh][vd][kd] */
+    float *out;                    /* [B][VH*VD] */
+    float *post, *gates, *W, *U, *Pm, *KdT, *gvec;
+    int t0, B, n_chunks, k_heads, v_heads;
+} Q35LinPrefill;
+/* workspace bytes, post included when with_post != 0 */
+void q35_lin_prefill_ws_bytes(int B, int k_heads, int v_heads, int with_post, size_t *bytes);
+hipError_t q35_lin_prefill(const Q35LinPrefill *p, hipStream_t stream);
+
 /* ---- GQA split-K decode (head_dim 256, 8 q heads per kv head) ---- */
 typedef struct Q35GqaDecode {
     const float *q_gate;           /* [H][2D] */

@@ -116,8 +116,11 @@ int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k,
                          const float *v, const uint16_t *qn_w,
                          const uint16_t *kn_w, float *attn_out);
 
-/* Prefill of B tokens of a delta-rule layer: the same results as B
- * ds4f_gpu_lin_decode calls in order (chunked form on the device). */
+/* Prefill of B tokens t0..t0+B-1 of a delta-rule layer: the results of B
+ * ds4f_gpu_lin_decode calls in order (up to fp32 rounding), computed in
+ * chunked WY form (64-token chunks, fp32 MFMA).  qkv [B][conv_rows] is
+ * mutated like the decode's; z / out [B][16*n_kv_heads*lin_vd], a / b
+ * [B][16*n_kv_heads]. */
 int ds4f_gpu_lin_prefill(int L, int t0, int B, float *qkv, const float *z,
                          const float *a, const float *b,
                          const uint16_t *conv_w, const float *A_log,
@@ -139,6 +142,14 @@ int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate,
                                const float *k, const float *v,
                                const uint16_t *qn_w, const uint16_t *kn_w,
                                float *attn_out, float *k_post, void *stream);
+/* Prefill of B tokens t0.. of a delta-rule layer (chunked form).  qkv_post
+ * [B][conv_rows] receives the post-conv, normed values (may be NULL).
+ * Allocates its workspace on first use or growth (not capturable then). */
+int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv,
+                               const float *z, const float *a, const float *b,
+                               const uint16_t *conv_w, const float *A_log,
+                               const uint16_t *dt_bias, const uint16_t *norm_w,
+                               float *out, float *qkv_post, void *stream);
 int ds4f_hip_lin_decode_async(int L, int token, const float *qkv,
                               const float *z, const float *a, const float *b,
                               const uint16_t *conv_w, const float *A_log,

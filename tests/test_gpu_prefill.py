@@ -118,3 +118,77 @@ def test_gqa_prefill_continues_a_cache():
     _say(f"chunked prefill + decode: worst max abs {worst:.3e}")
     assert worst <= ATOL
     ga.close()
+
+
+# ------------------------------------------------------------------ delta rule
+LG = W.LinGeom()
+STATE_RTOL = 1e-4
+
+
+def _lin_binding(max_tokens, t0, seed, zero_state):
+    cache = KvCache(1, max_tokens, with_kv=False)
+    if not zero_state:
+        cache.lin[0] = W.lin_state(LG, seed, 0)
+        cache.conv[0] = W.ring_from_history(LG, W.lin_conv_history(LG, seed, 0), t0)
+    ring, S0 = cache.conv[0].copy(), cache.lin[0].copy()
+    return GpuAttention([1], max_tokens, cache), cache, ring, S0, W.lin_weights(LG, seed, 0)
+
+
+def _lin_check(ga, cache, ring, S0, w, t0, qkv, z, a, b, what):
+    out, post = ga.lin_prefill(0, t0, qkv, z, a, b, w)
+    ref, rpost = O.lin_prefill(ring, S0, t0, qkv, z, a, b, w.conv_w, w.A_log, w.dt_bias,
+                               w.norm_w, LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+    ga.sync(0, to_host=True)
+    mx, rr = _err(out, ref)
+    pmx = _err(post, rpost)[0]
+    smx, srr = _err(cache.lin[0], S0)
+    _say(f"{what}: out max abs {mx:.3e} rel-rms {rr:.3e}; post {pmx:.3e}; "
+         f"state rel {srr:.3e} max abs {smx:.3e}")
+    assert mx <= ATOL
+    assert pmx <= 1e-5
+    assert srr <= STATE_RTOL
+    assert np.array_equal(cache.conv[0], ring)       # raw rows: exact
+    return out
+
+
+@pytest.mark.parametrize("T,t0", [(1, 0), (3, 0), (5, 0), (64, 0), (65, 0), (200, 0),
+                                  (1, 9), (2, 9), (130, 7)])
+def test_lin_prefill_chunked_vs_serial(T, t0):
+    """Chunk boundaries (64), ragged last chunks, B < 4 (ring keeps older
+    rows), a prefill continuing at an unaligned position with a past state
+    and conv history."""
+    ga, cache, ring, S0, w = _lin_binding(t0 + T + 8, t0, 11, zero_state=(t0 == 0))
+    qkv, z, a, b = W.lin_tokens(LG, T, 11)
+    _lin_check(ga, cache, ring, S0, w, t0, qkv, z, a, b, f"lin prefill T={T} t0={t0}")
+    ga.close()
+
+
+def test_lin_prefill_4096_zero_state():
+    """The 4096-token prefill from a zero state and zero conv ring (the
+    benchmark's delta prefill), against 4096 serial oracle bodies."""
+    T = 4096
+    _say("lin prefill T=4096 (oracle serial loop takes a while)")
+    ga, cache, ring, S0, w = _lin_binding(T + 8, 0, 0, zero_state=True)
+    qkv, z, a, b = W.lin_tokens(LG, T, 0)
+    _lin_check(ga, cache, ring, S0, w, 0, qkv, z, a, b, "lin prefill T=4096")
+    ga.close()
+
+
+def test_lin_prefill_then_decode():
+    """Prefill 100 tokens, then 37 more, then three decode steps, all against
+    the oracle's serial body on the same state."""
+    ga, cache, ring, S0, w = _lin_binding(256, 0, 13, zero_state=True)
+    qkv, z, a, b = W.lin_tokens(LG, 140, 13)
+    for t0, B in ((0, 100), (100, 37)):
+        sl = slice(t0, t0 + B)
+        _lin_check(ga, cache, ring, S0, w, t0, qkv[sl], z[sl], a[sl], b[sl],
+                   f"lin prefill t0={t0} B={B}")
+    worst = 0.0
+    for tok in range(137, 140):
+        out, _ = ga.lin_decode(0, tok, qkv[tok], z[tok], a[tok], b[tok], w)
+        ref, _ = O.lin_body(ring, S0, tok, qkv[tok], z[tok], a[tok], b[tok], w.conv_w, w.A_log,
+                            w.dt_bias, w.norm_w, LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+        worst = max(worst, _err(out, ref)[0])
+    _say(f"decode after chunked prefill: worst max abs {worst:.3e}")
+    assert worst <= ATOL
+    ga.close()
