@@ -192,7 +192,7 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
             p.vt[q35_v_index(g, p.token, d0 + e, p.t_tiles)] = q35_f2bf(vy[e]);
         }
     }
-    __syncthreads();
+    q35_lds_barrier();
 
     /* ---- main loop over 16-position sub-tiles w, w+4, ... of the chunk ---- */
     const int n = lane & 15, grp = lane >> 4, hq = n & 7;
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
             }
         }
     }
-    __syncthreads();
+    q35_lds_barrier();
 
     /* ---- merge the waves (and the new token): 8 x 5 factors once ---- */
     const int nsrc = last ? NW + 1 : NW;
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
         pml[t * 2] = M;
         pml[t * 2 + 1] = L;
     }
-    __syncthreads();
+    q35_lds_barrier();
     for (int e = t; e < G * D; e += NT) {
         const int hh = e / D, d = e % D;
         float o = sO[0][d * OS + hh] * sF[0][hh];
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(Q35GqaDecode p) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
     if (lane == 0) swave[0][w] = M;
-    __syncthreads();
+    q35_lds_barrier();
     M = fmaxf(fmaxf(swave[0][0], swave[0][1]), fmaxf(swave[0][2], swave[0][3]));
     const float f = (mc != -INFINITY) ? q35_exp(mc - M) : 0.0f;
     const float L0 = q35_wave_sum(lc * f);
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(Q35GqaDecode p) {
     for (int j = 0; j < MPER; j++)
         if (mv[j] != -INFINITY) o += ov[j] * q35_exp(mv[j] - M);
     sred[cg][dd] = o;
-    __syncthreads();
+    q35_lds_barrier();
     if (cg == 0) {
         const float L = (swave[1][0] + swave[1][1]) + (swave[1][2] + swave[1][3]);
         float ot = 0.0f;

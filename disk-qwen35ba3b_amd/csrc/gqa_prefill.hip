@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
 
     gload(0);
     sstore(0);
-    __syncthreads();
+    q35_lds_barrier();
     for (int kb = 0; kb < nkb; kb++) {
         const int buf = kb & 1;
         if (kb + 1 < nkb) gload(kb + 1);
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
         }
         if (kb + 1 < nkb) {
             sstore(buf ^ 1);
-            __syncthreads();
+            q35_lds_barrier();
         }
     }
 

@@ -96,7 +96,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         sgate[0] = expf(g);
         sgate[1] = beta;
     }
-    __syncthreads();
+    q35_lds_barrier();
     if (kind == 0 || kind == 1) {
 #pragma clang fp contract(off)
         double tot = kind == 0 ? sred[0] + sred[1] : sred[2] + sred[3];
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         sv[t - 2 * KD] = x;
         if (p.qkv_post) p.qkv_post[ch] = x;
     }
-    __syncthreads();
+    q35_lds_barrier();
 
     /* ---- gated delta rule on column j (src/attn_qwen.c:666-690) ---- */
     const float dec = sgate[0], beta = sgate[1];
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
 #pragma unroll
     for (int u = 0; u < 4; u++) sp[u] = s[u];
     if (il == 0) so[j] = o;
-    __syncthreads();
+    q35_lds_barrier();
 
     /* ---- RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749) ---- */
     if (t < VD) {
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         o2 = q35_wave_sum(o2);
         if ((t & 63) == 0) sred[t >> 6] = o2;
     }
-    __syncthreads();
+    q35_lds_barrier();
     if (t < VD) {
 #pragma clang fp contract(off)
         float r = sqrtf((float)((sred[0] + sred[1]) / (double)VD) + 1e-6f);

@@ -54,54 +54,61 @@ __device__ __forceinline__ float el(const float4 &v, int e) {
 }
 
 /* ---- 1. conv + SiLU, q/k norms, gates ------------------------------------ *
- * grid (rows / 512, B), 4 waves; wave w owns 128-channel group
- * 4*blockIdx.x + w (q heads, then k heads, then v heads), 2 channels a lane. */
+ * grid (rows / 512, ceil(B / 8)), 4 waves; wave w owns 128-channel group
+ * 4*blockIdx.x + w (q heads, then k heads, then v heads), 2 channels a
+ * lane, for 8 consecutive tokens: the 11 raw rows they tap are loaded once
+ * (a sliding window instead of 4 loads per output). */
+constexpr int CT = 8;
 __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
-    const int b = blockIdx.y, pos = p.t0 + b;
+    const int bb = blockIdx.y * CT;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
     const int grp = 4 * blockIdx.x + w;
     const int c0 = grp * 128 + 2 * lane;
 
-    float x0[4] = {0.f, 0.f, 0.f, 0.f}, x1[4] = {0.f, 0.f, 0.f, 0.f};
+    /* raw rows of positions t0+bb-3 .. t0+bb+CT-1 */
+    float2 xr[CT + 3];
 #pragma unroll
-    for (int k = 0; k < 3; k++) {
-        const int pp = pos - 3 + k;
+    for (int k = 0; k < CT + 3; k++) {
+        const int b = bb - 3 + k, pp = p.t0 + b;
         float2 v = make_float2(0.f, 0.f);
-        if (pp >= p.t0)
-            v = *reinterpret_cast<const float2 *>(p.qkv + (size_t)(b - 3 + k) * rows + c0);
-        else if (pp >= 0)
+        if (b >= 0 && b < p.B)
+            v = *reinterpret_cast<const float2 *>(p.qkv + (size_t)b * rows + c0);
+        else if (b < 0 && pp >= 0)
             v = *reinterpret_cast<const float2 *>(p.ring + (size_t)(pp & 3) * rows + c0);
-        x0[k] = v.x;
-        x1[k] = v.y;
-    }
-    {
-        const float2 v = *reinterpret_cast<const float2 *>(p.qkv + (size_t)b * rows + c0);
-        x0[3] = v.x;
-        x1[3] = v.y;
+        xr[k] = v;
     }
     const uint4 wv = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4);
-    float y0 = q35_conv_silu(x0, make_uint2(wv.x, wv.y), pos);
-    float y1 = q35_conv_silu(x1, make_uint2(wv.z, wv.w), pos);
-
-    if (grp < 2 * KH) {            /* q or k head: RMS norm (src/attn_qwen.c:522-538) */
+#pragma unroll
+    for (int j = 0; j < CT; j++) {
+        const int b = bb + j, pos = p.t0 + b;
+        if (b >= p.B) break;
+        const float x0[4] = {xr[j].x, xr[j + 1].x, xr[j + 2].x, xr[j + 3].x};
+        const float x1[4] = {xr[j].y, xr[j + 1].y, xr[j + 2].y, xr[j + 3].y};
+        float y0 = q35_conv_silu(x0, make_uint2(wv.x, wv.y), pos);
+        float y1 = q35_conv_silu(x1, make_uint2(wv.z, wv.w), pos);
+        if (grp < 2 * KH) {        /* q or k head: RMS norm (src/attn_qwen.c:522-538) */
 #pragma clang fp contract(off)
-        double ss = (double)y0 * y0 + (double)y1 * y1;
-        ss = q35_wave_sum(ss);
-        const float r = sqrtf((float)(ss / (double)KD) + 1e-6f);
-        const float scale = grp < KH ? 1.0f / (float)KD : 1.0f / sqrtf((float)KD);
-        y0 = y0 / r * scale;
-        y1 = y1 / r * scale;
+            double ss = (double)y0 * y0 + (double)y1 * y1;
+            ss = q35_wave_sum(ss);
+            const float r = sqrtf((float)(ss / (double)KD) + 1e-6f);
+            const float scale = grp < KH ? 1.0f / (float)KD : 1.0f / sqrtf((float)KD);
+            y0 = y0 / r * scale;
+            y1 = y1 / r * scale;
+        }
+        *reinterpret_cast<float2 *>(p.post + (size_t)b * rows + c0) = make_float2(y0, y1);
     }
-    *reinterpret_cast<float2 *>(p.post + (size_t)b * rows + c0) = make_float2(y0, y1);
 
-    if (blockIdx.x == 0 && threadIdx.x < VH) {
-        const int h = threadIdx.x;
-        float g, beta;
-        q35_lin_gates(p.a[(size_t)b * VH + h], p.b[(size_t)b * VH + h], p.A_log[h], p.dt_bias[h],
-                      &g, &beta);
-        *reinterpret_cast<float2 *>(p.gates + ((size_t)b * VH + h) * 2) = make_float2(g, beta);
+    if (blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < CT * VH; i += 256) {
+            const int b = bb + i / VH, h = i % VH;
+            if (b >= p.B) break;
+            float g, beta;
+            q35_lin_gates(p.a[(size_t)b * VH + h], p.b[(size_t)b * VH + h], p.A_log[h],
+                          p.dt_bias[h], &g, &beta);
+            *reinterpret_cast<float2 *>(p.gates + ((size_t)b * VH + h) * 2) = make_float2(g, beta);
+        }
     }
 }
 
@@ -167,7 +174,7 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         *reinterpret_cast<float4 *>(&sK[r * XS + c4]) = kv;
         *reinterpret_cast<float4 *>(&sQA[r * XS + c4]) = qv;
     }
-    __syncthreads();
+    q35_lds_barrier();
 
     /* K K^T and Q K^T, the 10 lower 16x16 tiles of each: tile n (0..19),
      * wave w takes n = w, w+4, ..., w+16.  Lane l holds rows 4*(l/16)+i. */
@@ -188,8 +195,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         }
         res[k] = acc;
     }
-    __syncthreads();                       /* Q no longer read: its LDS becomes A */
-    float *sA = sQA;
+    q35_lds_barrier();                       /* Q no longer read: its LDS becomes A^T */
+    float *sAT = sQA;
     float *Pm = p.Pm + ((size_t)c * VH + h) * C * C;
 #pragma unroll
     for (int k = 0; k < 5; k++) {
@@ -202,15 +209,18 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
             const int r = 16 * tr + 4 * lq + i;
             const float dec = expf((float)(sG[r] - sG[s]));
             if (n < 10)
-                sA[r * AS + s] = s < r ? sBeta[r] * dec * res[k][i] : 0.0f;
+                sAT[s * AS + r] = s < r ? sBeta[r] * dec * res[k][i] : 0.0f;
             else
                 Pm[r * C + s] = s <= r ? dec * res[k][i] : 0.0f;
         }
     }
-    __syncthreads();
+    q35_lds_barrier();
 
     /* forward substitution, one right-hand-side column a thread:
-     * columns 0..127 -> W (rhs beta_r exp(G_r) k_r), 128..255 -> U (beta_r v_r) */
+     * columns 0..127 -> W (rhs beta_r exp(G_r) k_r), 128..255 -> U (beta_r v_r).
+     * Right-looking: once x_s is final it is applied to every later row, so
+     * each step is up to 63 independent FMAs (column s of A is row s of
+     * A^T, read four entries at a time). */
     float x[C];
     if (t < KD) {
 #pragma unroll
@@ -221,11 +231,15 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         for (int r = 0; r < C; r++) x[r] = r < nv ? sBeta[r] * vcol[(size_t)r * rows] : 0.0f;
     }
 #pragma unroll
-    for (int r = 1; r < C; r++) {
-        float acc = x[r];
+    for (int s = 0; s < C - 1; s++) {
+        const float xs = x[s];
 #pragma unroll
-        for (int s = 0; s < r; s++) acc = fmaf(-sA[r * AS + s], x[s], acc);
-        x[r] = acc;
+        for (int r4 = ((s + 1) >> 2) << 2; r4 < C; r4 += 4) {
+            const float4 a4 = *reinterpret_cast<const float4 *>(&sAT[s * AS + r4]);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (r4 + e > s) x[r4 + e] = fmaf(-el(a4, e), xs, x[r4 + e]);
+        }
     }
     float *dst = (t < KD ? p.W : p.U) + ((size_t)c * VH + h) * C * KD + (t & (KD - 1));
 #pragma unroll
@@ -246,118 +260,151 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  * 32w..32w+31 of the state block.  Workgroup n runs head
  * (n & 7) + 8 (n >> 6), block (n >> 3) & 7: the 8 blocks of a head share an
  * XCD (workgroups are dealt round-robin over the 8 XCDs), so the chunk
- * operands they all read stay in one L2. */
+ * operands they all read stay in one L2.  The operands of chunk c+1 (they
+ * do not depend on the state) are loaded into a second register set while
+ * chunk c computes. */
+struct ScanOps {
+    float4 wa[8], qa[8], pa[4], ka[2][4];
+    float u[4], gq[4], gc;
+};
+
+struct ScanCtx {
+    int h, jb, kh, w, l16, lq, rows, VH;
+};
+
+__device__ __forceinline__ void scan_load(ScanOps &o, const Q35LinPrefill &p, const ScanCtx &x,
+                                          int c) {
+    const int b0 = c * C, nv = min(C, p.B - b0);
+    const size_t ch = (size_t)c * x.VH + x.h;
+    const float *Wc = p.W + ch * C * KD, *Uc = p.U + ch * C * VD;
+    const float *Pc = p.Pm + ch * C * C, *Kc = p.KdT + ch * KD * C;
+    const float *gv = p.gvec + ch * Q35_LIN_GVEC;
+    const int row = 16 * x.w + x.l16;
+#pragma unroll
+    for (int blk = 0; blk < 8; blk++)
+        o.wa[blk] = *reinterpret_cast<const float4 *>(Wc + (size_t)row * KD + 16 * blk + 4 * x.lq);
+    /* every load is unconditional, so the compiler can count the loads in
+     * flight exactly and wait for this set only.  Rows past the batch read
+     * the last row's q: q row t only feeds output row t, which is not
+     * stored for those rows. */
+    const float *qrow = p.post + (size_t)(b0 + min(row, nv - 1)) * x.rows + x.kh * KD + 4 * x.lq;
+#pragma unroll
+    for (int blk = 0; blk < 8; blk++) o.qa[blk] = *reinterpret_cast<const float4 *>(qrow + 16 * blk);
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++)   /* key blocks past the diagonal: unused */
+        o.pa[blk] = *reinterpret_cast<const float4 *>(Pc + (size_t)row * C + 16 * blk + 4 * x.lq);
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++)
+            o.ka[tt][blk] = *reinterpret_cast<const float4 *>(
+                Kc + (size_t)(16 * (2 * x.w + tt) + x.l16) * C + 16 * blk + 4 * x.lq);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * x.w + 4 * x.lq + i;
+        o.u[i] = Uc[(size_t)r * VD + 16 * x.jb + x.l16];
+        o.gq[i] = gv[r];
+    }
+    o.gc = gv[2 * C];
+}
+
+__device__ __forceinline__ void scan_step(const ScanOps &o, const Q35LinPrefill &p,
+                                          const ScanCtx &x, int c, float *sS, float *sD) {
+    const int b0 = c * C, nv = min(C, p.B - b0);
+    const int w = x.w, l16 = x.l16, lq = x.lq;
+
+    /* W S0 and Q S0 (rows 16w.., all 128 key rows of the block) */
+    f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, aq = aw;
+#pragma unroll
+    for (int blk = 0; blk < 8; blk++) {
+        const float4 sb = *reinterpret_cast<const float4 *>(&sS[l16 * XS + 16 * blk + 4 * lq]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            aw = mfma4(el(o.wa[blk], e), el(sb, e), aw);
+            aq = mfma4(el(o.qa[blk], e), el(sb, e), aq);
+        }
+    }
+    float4 dl;
+    dl.x = o.u[0] - aw[0];
+    dl.y = o.u[1] - aw[1];
+    dl.z = o.u[2] - aw[2];
+    dl.w = o.u[3] - aw[3];
+    *reinterpret_cast<float4 *>(&sD[l16 * AS + 16 * w + 4 * lq]) = dl;
+    f32x4_t ao;
+#pragma unroll
+    for (int i = 0; i < 4; i++) ao[i] = o.gq[i] * aq[i];
+    q35_lds_barrier();
+
+    float4 db[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++)
+        db[blk] = *reinterpret_cast<const float4 *>(&sD[l16 * AS + 16 * blk + 4 * lq]);
+    /* O += Pm Delta (causal: key blocks 0..w) */
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) {
+        if (blk <= w) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) ao = mfma4(el(o.pa[blk], e), el(db[blk], e), ao);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * w + 4 * lq + i;
+        if (r < nv) p.out[((size_t)(b0 + r) * x.VH + x.h) * VD + 16 * x.jb + l16] = ao[i];
+    }
+
+    /* S_end = exp(G_C) S0 + Kd^T Delta on key rows 32w..32w+31 */
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        float *sp = &sS[l16 * XS + 16 * (2 * w + tt) + 4 * lq];
+        const float4 s0 = *reinterpret_cast<const float4 *>(sp);
+        f32x4_t acc = {o.gc * s0.x, o.gc * s0.y, o.gc * s0.z, o.gc * s0.w};
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc = mfma4(el(o.ka[tt][blk], e), el(db[blk], e), acc);
+        *reinterpret_cast<float4 *>(sp) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+    q35_lds_barrier();
+}
+
 __global__ __launch_bounds__(256) void scan_kernel(Q35LinPrefill p) {
     const int n = blockIdx.x;
-    const int h = (n & 7) + 8 * (n >> 6), jb = (n >> 3) & 7, kh = h >> 1;
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int l16 = lane & 15, lq = lane >> 4;
-    const int KH = p.k_heads, VH = p.v_heads;
-    const int rows = 2 * KH * KD + VH * VD;
+    ScanCtx x;
+    x.h = (n & 7) + 8 * (n >> 6);
+    x.jb = (n >> 3) & 7;
+    x.kh = x.h >> 1;
+    const int t = threadIdx.x, lane = t & 63;
+    x.w = t >> 6;
+    x.l16 = lane & 15;
+    x.lq = lane >> 4;
+    x.VH = p.v_heads;
+    x.rows = 2 * p.k_heads * KD + p.v_heads * VD;
 
     __shared__ __align__(16) float sS[16 * XS];   /* state block, [j][i] */
     __shared__ __align__(16) float sD[16 * AS];   /* Delta, [j][t] */
 
-    float *state = p.state + ((size_t)h * VD + 16 * jb) * KD;
+    float *state = p.state + ((size_t)x.h * VD + 16 * x.jb) * KD;
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int idx = u * 256 + t, j = idx >> 5, i4 = (idx & 31) * 4;
         *reinterpret_cast<float4 *>(&sS[j * XS + i4]) =
             *reinterpret_cast<const float4 *>(state + (size_t)j * KD + i4);
     }
-    __syncthreads();
+    ScanOps A, B;
+    scan_load(A, p, x, 0);
+    q35_lds_barrier();
 
-    for (int c = 0; c < p.n_chunks; c++) {
-        const int b0 = c * C, nv = min(C, p.B - b0);
-        const size_t ch = (size_t)c * VH + h;
-        const float *Wc = p.W + ch * C * KD, *Uc = p.U + ch * C * VD;
-        const float *Pc = p.Pm + ch * C * C, *Kc = p.KdT + ch * KD * C;
-        const float *gv = p.gvec + ch * Q35_LIN_GVEC;
-
-        /* operands of this chunk (they do not depend on the state) */
-        const int row = 16 * w + l16;
-        float4 wa[8], qa[8], pa[4], ka[2][4];
-#pragma unroll
-        for (int blk = 0; blk < 8; blk++)
-            wa[blk] = *reinterpret_cast<const float4 *>(Wc + (size_t)row * KD + 16 * blk + 4 * lq);
-        const float *qrow = p.post + (size_t)(b0 + row) * rows + kh * KD + 4 * lq;
-#pragma unroll
-        for (int blk = 0; blk < 8; blk++)
-            qa[blk] = row < nv ? *reinterpret_cast<const float4 *>(qrow + 16 * blk)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int blk = 0; blk < 4; blk++)
-            pa[blk] = blk <= w ? *reinterpret_cast<const float4 *>(Pc + (size_t)row * C + 16 * blk + 4 * lq)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-            for (int blk = 0; blk < 4; blk++)
-                ka[tt][blk] = *reinterpret_cast<const float4 *>(
-                    Kc + (size_t)(16 * (2 * w + tt) + l16) * C + 16 * blk + 4 * lq);
-        float u[4], gq[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 16 * w + 4 * lq + i;
-            u[i] = Uc[(size_t)r * VD + 16 * jb + l16];
-            gq[i] = gv[r];
-        }
-        const float gc = gv[2 * C];
-
-        /* W S0 and Q S0 (rows 16w.., all 128 key rows of the block) */
-        f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, aq = aw;
-#pragma unroll
-        for (int blk = 0; blk < 8; blk++) {
-            const float4 sb = *reinterpret_cast<const float4 *>(&sS[l16 * XS + 16 * blk + 4 * lq]);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                aw = mfma4(el(wa[blk], e), el(sb, e), aw);
-                aq = mfma4(el(qa[blk], e), el(sb, e), aq);
-            }
-        }
-        float4 dl;
-        dl.x = u[0] - aw[0];
-        dl.y = u[1] - aw[1];
-        dl.z = u[2] - aw[2];
-        dl.w = u[3] - aw[3];
-        *reinterpret_cast<float4 *>(&sD[l16 * AS + 16 * w + 4 * lq]) = dl;
-        f32x4_t ao;
-#pragma unroll
-        for (int i = 0; i < 4; i++) ao[i] = gq[i] * aq[i];
-        __syncthreads();
-
-        /* O += Pm Delta (causal: key blocks 0..w) */
-#pragma unroll
-        for (int blk = 0; blk < 4; blk++) {
-            if (blk <= w) {
-                const float4 db = *reinterpret_cast<const float4 *>(&sD[l16 * AS + 16 * blk + 4 * lq]);
-#pragma unroll
-                for (int e = 0; e < 4; e++) ao = mfma4(el(pa[blk], e), el(db, e), ao);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 16 * w + 4 * lq + i;
-            if (r < nv) p.out[((size_t)(b0 + r) * VH + h) * VD + 16 * jb + l16] = ao[i];
-        }
-
-        /* S_end = exp(G_C) S0 + Kd^T Delta on key rows 32w..32w+31 */
-        float4 db[4];
-#pragma unroll
-        for (int blk = 0; blk < 4; blk++)
-            db[blk] = *reinterpret_cast<const float4 *>(&sD[l16 * AS + 16 * blk + 4 * lq]);
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            float *sp = &sS[l16 * XS + 16 * (2 * w + tt) + 4 * lq];
-            const float4 s0 = *reinterpret_cast<const float4 *>(sp);
-            f32x4_t acc = {gc * s0.x, gc * s0.y, gc * s0.z, gc * s0.w};
-#pragma unroll
-            for (int blk = 0; blk < 4; blk++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc = mfma4(el(ka[tt][blk], e), el(db[blk], e), acc);
-            *reinterpret_cast<float4 *>(sp) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        }
-        __syncthreads();
+    /* the prefetch is unconditional (past the end it reloads the last chunk,
+     * unused): a conditional one would leave the compiler unable to count
+     * the loads in flight, and it would wait for all of them */
+    const int last = p.n_chunks - 1;
+    for (int c = 0; c < p.n_chunks; c += 2) {
+        scan_load(B, p, x, min(c + 1, last));
+        scan_step(A, p, x, c, sS, sD);
+        if (c + 1 > last) break;
+        scan_load(A, p, x, min(c + 2, last));
+        scan_step(B, p, x, c + 1, sS, sD);
     }
 
 #pragma unroll
@@ -413,7 +460,7 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     if (p.B < 1 || p.t0 < 0 || p.v_heads != 2 * p.k_heads || p.v_heads % 8 != 0 ||
         rows % 512 != 0 || p.n_chunks != (p.B + C - 1) / C)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(conv_kernel, dim3(rows / 512, p.B), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(conv_kernel, dim3(rows / 512, (p.B + CT - 1) / CT), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nr = p.B < 4 ? p.B : 4;

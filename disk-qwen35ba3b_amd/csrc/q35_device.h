@@ -82,6 +82,19 @@ __device__ __forceinline__ T q35_wave_sum(T v) {
     return (q35_readlane(v, 0) + q35_readlane(v, 16)) + (q35_readlane(v, 32) + q35_readlane(v, 48));
 }
 
+/* Workgroup barrier that orders LDS only.  __syncthreads() carries a
+ * workgroup-scope fence over all address spaces, which gfx950 implements as
+ * s_waitcnt vmcnt(0) lgkmcnt(0) before s_barrier: every global load in
+ * flight (a prefetch of the next tile) would be drained at each barrier.
+ * Where waves exchange data through LDS alone, this barrier waits for LDS
+ * operations only (s_waitcnt lgkmcnt(0); s_barrier) and global loads stay
+ * in flight across it. */
+__device__ __forceinline__ void q35_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 /* exp on the hardware 2^x instruction (v_exp_f32), ~1e-7 relative error:
  * used for softmax weights, whose reference-order expf only matters to
  * float rounding. */
