@@ -20,6 +20,10 @@ host, one thread, on a bounded sample of the same steps).
 Other workloads (one JSON line each, same fields):
   gqa_prefill   causal GQA prefill of --tokens (4096) tokens, one layer,
                 bf16-valued q|gate/k/v N(0,1); MFMA roofline.
+  hbm_copy      an elementwise copy (dst = src * 1) of a 1 GiB fp32 buffer:
+                the measured HBM ceiling, and the known-size kernel that
+                scales the FETCH_SIZE / WRITE_SIZE counters of the traffic
+                profiles.
   lin_prefill   gated delta-rule prefill of --tokens (4096) tokens, one
                 layer, zero state and conv ring, fp32 qkv/z/a/b N(0,1);
                 chunked form on fp32 MFMA, roofline against the fp32 MFMA
@@ -70,7 +74,7 @@ def main() -> int:
                     help="CPU-baseline sample budget (whole steps, at least one)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill",
-                                                                    "lin_prefill"])
+                                                                    "lin_prefill", "hbm_copy"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     args = ap.parse_args()
 
@@ -82,6 +86,8 @@ def main() -> int:
         return run_gqa_prefill(args)
     if args.workload == "lin_prefill":
         return run_lin_prefill(args)
+    if args.workload == "hbm_copy":
+        return run_hbm_copy(args)
     return run_stack_decode(args)
 
 
@@ -229,10 +235,7 @@ def run_stack_decode(args) -> int:
     del gq_graph
     gqa_bytes = sum(gqa_layer_bytes(N + s) for s in range(WU, T)) / K
     achieved = gqa_bytes / (gqa_us * 1e-6) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"gqa_decode_ctx{N}_traffic.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("bytes_per_launch")
+    traffic = load_traffic(f"gqa_decode_ctx{N}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                 "kernel": "gqa decode = gqa_split_kernel + gqa_merge_kernel",
@@ -346,7 +349,8 @@ def run_gqa_prefill(args) -> int:
     flops = 4.0 * gq.heads * gq.head_dim * T * (T + 1) / 2
     tflops = flops / (op_us * 1e-6) / 1e12
     roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                "traffic": load_traffic(f"gqa_prefill_t{T}"),
                 "kernel": "gqa prefill = prep_kernel + prefix_kernel + attn_kernel (fp16 MFMA)",
                 "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops}
 
@@ -384,6 +388,51 @@ def run_gqa_prefill(args) -> int:
             "config": {"workload": "gqa causal prefill", "tokens": T, "t0": 0, "layers": 1},
             "wall_ms_per_step": round(sec / K * 1e3, 4),
             "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE counter
+    runs summarised in profiles/<name>_traffic.json (null when absent)."""
+    tpath = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if os.path.exists(tpath):
+        return json.load(open(tpath)).get("bytes_per_launch")
+    return None
+
+
+def run_hbm_copy(args) -> int:
+    """dst = src * 1 over a 1 GiB fp32 buffer: 1 GiB read + 1 GiB written
+    per launch."""
+    import torch
+
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    n = (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    K, WU = max(1, min(args.steps, 50)), max(1, min(args.warmup, 5))
+    for _ in range(WU):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(K):
+        torch.mul(src, 1.0, out=dst)
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / K
+    gbps = 2.0 * n * 4 / (us * 1e-6) / 1e9
+    line = {"metric": "HBM copy GB/s (1 GiB fp32, read + write)", "value": round(gbps, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": WU,
+            "ms_per_step": round(us / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (ones)",
+            "config": {"workload": "hbm copy", "bytes_read": n * 4, "bytes_written": n * 4},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                         "traffic": None, "kernel": "torch elementwise mul (copy)",
+                         "launches": K, "us_per_launch": round(us, 2)},
+            "cpu_baseline": None}
     print(json.dumps(line), flush=True)
     return 0
 
@@ -456,7 +505,7 @@ def run_lin_prefill(args) -> int:
     tflops = flops / (op_us * 1e-6) / 1e12
     roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4),
-                "traffic": None,
+                "traffic": load_traffic(f"lin_prefill_t{T}"),
                 "kernel": "delta prefill = conv + ring + chunk + scan + gnorm kernels "
                           "(fp32 MFMA), state reset included",
                 "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops}
