@@ -11,17 +11,21 @@
  * 2. prefix: cache rows of positions before t0 (earlier chunks) into the
  *            fp16 key / value workspaces; zero padding rows (only launched
  *            when there are such rows).
- * 3. attn:   grid = (16-position q blocks, kv heads), 4 waves.  A workgroup
- *            serves the 8 q heads of its kv head (wave w: heads 2w, 2w+1 x
- *            16 positions = 32 columns), so every K / V tile staged in LDS
- *            feeds 128 query rows.  Per 32-key block:
+ * 3. attn:   grid = (pairs of 16-position q blocks, kv heads), 4 waves.  A
+ *            workgroup serves the 8 q heads of its kv head (wave w: heads
+ *            2w, 2w+1 x 16 positions = 32 columns), so every K / V tile
+ *            staged in LDS feeds 128 query rows.  Per 32-key block:
  *              S^T[32 key][32 q] = K Q^T   (16 x v_mfma_f32_32x32x16_f16),
  *              online softmax per column (rescaled only when a column max
- *              grows by more than 8, which keeps P <= e^8 in fp16),
+ *              grows by more than 8 in scaled units, which keeps P <= e^8
+ *              in fp16),
  *              O^T[256][32 q] += V^T P^T  (16 x 32x32x16 f16; the S^T
  *              accumulator registers are P's B operand as they stand, the
  *              value tile is stored in the matching key order).
- *            Output O / l times sigmoid(gate), fp32.
+ *            Output O / l times sigmoid(gate), fp32.  K / V tiles move
+ *            global -> registers (buffer loads, one tile ahead) -> padded
+ *            LDS (two stages); each workgroup runs a long and a short q
+ *            block so every workgroup carries the same causal work.
  * Operands are fp16 (11-bit mantissa): a single MFMA pass keeps the
  * outputs within the parity bar (max abs error ~1e-3 against the fp32
  * reference at T = 4096), where bf16 operands would not.
@@ -35,10 +39,11 @@ typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
 namespace {
 
 constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
-constexpr int KPAD = D + 8;     /* LDS key-row stride (halfs): 528 B */
-constexpr int VPAD = 32 + 8;    /* LDS value-row stride (halfs): 80 B, conflict-free */
-constexpr float SCALE = 0.0625f;
-constexpr float RESCALE_MARGIN = 8.0f;
+constexpr float SCALE = 0.0625f;                        /* 1/sqrt(256) */
+constexpr float RESCALE_MARGIN = 8.0f;                  /* in scaled units */
+constexpr float EXP_K = SCALE * 1.4426950408889634f;    /* exp(SCALE x) = 2^(EXP_K x) */
+
+__device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ uint16_t f16_bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
@@ -153,20 +158,85 @@ __global__ void qpad_kernel(Q35GqaPrefill p, int n_pad) {
     p.qw[((((size_t)g * p.nqb + (qpos >> 4)) * G + hl) * 16 + (qpos & 15)) * D + d] = 0;
 }
 
+
+
+/* LDS tiles of one 32-key block.  Rows are padded by one 16-byte granule
+ * so the MFMA operand reads are conflict-free and take one address
+ * register plus immediate offsets:
+ *   K tile: 32 key rows x 33 granules (528 B; granule 32 unused),
+ *   V tile: 256 dim rows x 5 granules (80 B; granule 4 unused). */
+constexpr int KROW = 33, VROW = 5;
+constexpr int KTILE = 32 * KROW * 8, VTILE = D * VROW * 8;      /* halfs */
+
+/* dword 3 of a raw buffer resource on gfx9-family GPUs (no format
+ * conversion, range checking against num_records) */
+constexpr int Q35_BUF_DW3 = 0x00020000;
+
+/* Instruction order for a block of 16 MFMAs fed by 16 LDS fragment reads:
+ * 8 reads, then (4 MFMAs, 4 reads) x 3, then 4 MFMAs, so a batch of reads
+ * is always in flight under the previous batch's MFMAs.  Left to itself
+ * the scheduler minimises registers and waits on each read. */
+__device__ __forceinline__ void sched_reads_ahead() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    /* DS reads */
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  /* MFMA */
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+}
+
+/* max of v over the two 32-lane halves (lanes l and l ^ 32), on the
+ * cross-half swap of gfx950 instead of an LDS permute */
+__device__ __forceinline__ float half_pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
+}
+
+/* Causal work per q block grows with its position, so workgroup x runs
+ * the pair of q blocks (nqb-1-x, x): the longest with the shortest, equal
+ * total work for every workgroup whatever CU it lands on. */
 __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
     const int g = blockIdx.y;
-    const int qb = p.nqb - 1 - (int)blockIdx.x;          /* longest key range first */
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int h = lane >> 5, col = lane & 31;
-    const int q0 = p.t0 + 16 * qb;
-    const int qpos = q0 + (col & 15);
     const int hl = 2 * w + (col >> 4);
     const int end = p.t0 + p.B;
+
+    __shared__ __align__(16) _Float16 sK[2][KTILE];
+    __shared__ __align__(16) _Float16 sV[2][VTILE];
+
+    /* staging: thread t moves granules t + 256 j (j < 4) of the K tile
+     * (row (t + 256 j) / 32) and of the V tile (row (t + 256 j) / 4) through
+     * registers.  Buffer loads on a range-checked resource per kv head: the
+     * tile offset is the scalar offset, the lane's offset a loop-invariant
+     * VGPR. */
+    const uint32_t tile_bytes = 32 * D * 2;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(p.kw + (size_t)g * p.kbt * 32 * D), 0, p.kbt * tile_bytes, Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(p.vw + (size_t)g * p.kbt * D * 32), 0, p.kbt * tile_bytes, Q35_BUF_DW3);
+    uint32_t kgo[4], vgo[4];
+    int klo[4], vlo[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int gi = t + 256 * j;
+        kgo[j] = (uint32_t)gi * 16u;                 /* K tile: 32 granules a row */
+        vgo[j] = (uint32_t)gi * 16u;                 /* V tile: 4 granules a row */
+        klo[j] = ((gi >> 5) * KROW + (gi & 31)) * 8;
+        vlo[j] = ((gi >> 2) * VROW + (gi & 3)) * 8;
+    }
+    const int kbase = (col * KROW + h) * 8;          /* + 16 ks halfs */
+    const int vbase = (col * VROW + h) * 8;          /* + dt * 32 rows + 16 ks halfs */
+    typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+
+  for (int item = 0; item < 2; item++) {
+    const int qb = item == 0 ? p.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    if (item == 1 && qb >= p.nqb - 1 - (int)blockIdx.x) break;   /* odd middle block */
+    const int q0 = p.t0 + 16 * qb;
+    const int qpos = q0 + (col & 15);
     const int n_keys = min(q0 + 16, end);
     const int nkb = (n_keys + 31) >> 5;
-
-    __shared__ _Float16 sK[2][32 * KPAD];
-    __shared__ _Float16 sV[2][D * VPAD];
 
     /* Q^T as the B operand for the wave's 32 columns, all 16 k-steps */
     const uint16_t *qrow = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + (col & 15)) * D;
@@ -175,28 +245,6 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
     for (int ks = 0; ks < 16; ks++)
         qop[ks] = *reinterpret_cast<const f16x8_t *>(qrow + 16 * ks + 8 * h);
 
-    /* staging: thread t copies key row t>>3 (64 B at column chunk t&7) and
-     * value row t (its 32 keys, 64 B) of a block */
-    uint4 stK[4], stV[4];
-    const uint16_t *kwb = p.kw + (size_t)g * p.kbt * 32 * D + (t >> 3) * D + (t & 7) * 32;
-    const uint16_t *vwb = p.vw + (size_t)g * p.kbt * D * 32 + t * 32;
-    auto gload = [&](int kb) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            stK[u] = *reinterpret_cast<const uint4 *>(kwb + (size_t)kb * 32 * D + u * 8);
-            stV[u] = *reinterpret_cast<const uint4 *>(vwb + (size_t)kb * D * 32 + u * 8);
-        }
-    };
-    auto sstore = [&](int buf) {
-        _Float16 *kd = &sK[buf][(t >> 3) * KPAD + (t & 7) * 32];
-        _Float16 *vd = &sV[buf][t * VPAD];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            *reinterpret_cast<uint4 *>(kd + u * 8) = stK[u];
-            *reinterpret_cast<uint4 *>(vd + u * 8) = stV[u];
-        }
-    };
-
     f32x16_t acc[8];
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
@@ -204,62 +252,135 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
         for (int i = 0; i < 16; i++) acc[dt][i] = 0.0f;
     float m_used = -INFINITY, l_run = 0.0f;
 
-    gload(0);
-    sstore(0);
+    /* tile 0 into stage 0, tile 1 into the staging registers; every load is
+     * unconditional (a tile index past the end is clamped and its copy is
+     * never read), so the compiler waits on exactly the loads it needs */
+    u32x4_t stg[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        stg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, kgo[j], 0, 0);
+        stg[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vgo[j], 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        *reinterpret_cast<u32x4_t *>(&sK[0][klo[j]]) = stg[j];
+        *reinterpret_cast<u32x4_t *>(&sV[0][vlo[j]]) = stg[4 + j];
+    }
+    {
+        const uint32_t so = (uint32_t)min(1, nkb - 1) * tile_bytes;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            stg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, kgo[j], so, 0);
+            stg[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vgo[j], so, 0);
+        }
+    }
     q35_lds_barrier();
+
     for (int kb = 0; kb < nkb; kb++) {
         const int buf = kb & 1;
-        if (kb + 1 < nkb) gload(kb + 1);
         /* S^T = K Q^T: lane holds column col, keys 32kb + 8j + 4h + i' */
         f32x16_t s;
 #pragma unroll
         for (int i = 0; i < 16; i++) s[i] = 0.0f;
+        {
+            const _Float16 *kp = &sK[buf][kbase];
+            f16x8_t ka[2][4];
 #pragma unroll
-        for (int ks = 0; ks < 16; ks++) {
-            const f16x8_t a = *reinterpret_cast<const f16x8_t *>(&sK[buf][col * KPAD + 16 * ks + 8 * h]);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[ks], s, 0, 0, 0);
+            for (int u = 0; u < 4; u++) ka[0][u] = *reinterpret_cast<const f16x8_t *>(kp + 16 * u);
+#pragma unroll
+            for (int bq = 0; bq < 4; bq++) {
+                if (bq < 3) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        ka[(bq + 1) & 1][u] =
+                            *reinterpret_cast<const f16x8_t *>(kp + 16 * (4 * (bq + 1) + u));
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[bq & 1][u], qop[4 * bq + u], s, 0, 0, 0);
+            }
+            sched_reads_ahead();
         }
+        /* element i is key 32kb + 8(i/4) + 4h + i%4: causal (key <= qpos) and
+         * inside the batch (key < end) as one per-lane bound on the
+         * compile-time offset 8(i/4) + i%4.  Scores stay unscaled here; the
+         * 1/16 scale rides in the exponent's multiplier. */
+        const int lim = min(qpos + 1, end) - 32 * kb - 4 * h;
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int key = 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
-            const float v = (key <= qpos && key < end) ? s[i] * SCALE : -INFINITY;
+            const float v = (8 * (i >> 2) + (i & 3)) < lim ? s[i] : -INFINITY;
             s[i] = v;
             mx = fmaxf(mx, v);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const bool need = mx > m_used + RESCALE_MARGIN;
+        mx = half_pair_max(mx);
+        const bool need = mx > m_used + RESCALE_MARGIN / SCALE;
         if (__any(need)) {
             const float m_new = need ? mx : m_used;
-            const float alpha = q35_exp(m_used - m_new);   /* -inf -> 0 on first use */
+            const float alpha = exp2f_fast((m_used - m_new) * EXP_K);   /* -inf -> 0 on first use */
             l_run *= alpha;
+            /* one 16-register tile at a time: the accumulators live in
+             * AGPRs and this rare path must not hold all 128 in VGPRs */
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) acc[dt] *= alpha;
+            for (int dt = 0; dt < 8; dt++) {
+                acc[dt] *= alpha;
+                __builtin_amdgcn_sched_barrier(0);
+            }
             m_used = m_new;
         }
         f16x8_t pb[2];
         float ps = 0.0f;
+        const float mk = m_used * EXP_K;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float pv = q35_exp(s[i] - m_used);
+            const float pv = exp2f_fast(fmaf(s[i], EXP_K, -mk));
             ps += pv;
             pb[i >> 3][i & 7] = (_Float16)pv;
         }
         l_run += ps;
-        /* O^T += V^T P^T */
+        /* O^T += V^T P^T, V fragments in batches of 4 (two dim tiles) */
+        {
+            const _Float16 *vp = &sV[buf][vbase];
+            f16x8_t va[2][4];
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
+            for (int u = 0; u < 4; u++)
+                va[0][u] = *reinterpret_cast<const f16x8_t *>(vp + (u >> 1) * 32 * VROW * 8 + 16 * (u & 1));
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                const f16x8_t a = *reinterpret_cast<const f16x8_t *>(
-                    &sV[buf][(32 * dt + col) * VPAD + 16 * ks + 8 * h]);
-                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[ks], acc[dt], 0, 0, 0);
+            for (int bq = 0; bq < 4; bq++) {
+                if (bq < 3) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int dt = 2 * (bq + 1) + (u >> 1);
+                        va[(bq + 1) & 1][u] =
+                            *reinterpret_cast<const f16x8_t *>(vp + dt * 32 * VROW * 8 + 16 * (u & 1));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int dt = 2 * bq + (u >> 1);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bq & 1][u], pb[u & 1], acc[dt],
+                                                                     0, 0, 0);
+                }
+            }
+            sched_reads_ahead();
+        }
+        /* staged tile kb+1 into the other stage (every wave finished tile
+         * kb-1, its previous occupant, before the last barrier), then the
+         * loads of tile kb+2 */
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            *reinterpret_cast<u32x4_t *>(&sK[buf ^ 1][klo[j]]) = stg[j];
+            *reinterpret_cast<u32x4_t *>(&sV[buf ^ 1][vlo[j]]) = stg[4 + j];
+        }
+        {
+            const uint32_t so = (uint32_t)min(kb + 2, nkb - 1) * tile_bytes;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                stg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, kgo[j], so, 0);
+                stg[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vgo[j], so, 0);
             }
         }
-        if (kb + 1 < nkb) {
-            sstore(buf ^ 1);
-            q35_lds_barrier();
-        }
+        q35_lds_barrier();
     }
 
     const float L = l_run + __shfl_xor(l_run, 32);
@@ -283,6 +404,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
             }
         }
     }
+  }
 }
 
 }  // namespace
@@ -319,6 +441,6 @@ extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stre
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(attn_kernel, dim3(p.nqb, p.kv_heads), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(attn_kernel, dim3((p.nqb + 1) / 2, p.kv_heads), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
