@@ -20,6 +20,11 @@ host, one thread, on a bounded sample of the same steps).
 Other workloads (one JSON line each, same fields):
   gqa_prefill   causal GQA prefill of --tokens (4096) tokens, one layer,
                 bf16-valued q|gate/k/v N(0,1); MFMA roofline.
+  gqa_decode    one GQA decode call at n_past = --npast (4096), rotated over
+                --rotate (128) bound layers so the KV read (1.08 GB in all)
+                comes from HBM, not the 256 MB MALL; HBM roofline.
+  lin_decode    one delta-rule decode call, rotated over --rotate (256)
+                bound layers (0.5 GB of state); HBM roofline.
   hbm_copy      an elementwise copy (dst = src * 1) of a 1 GiB fp32 buffer:
                 the measured HBM ceiling, and the known-size kernel that
                 scales the FETCH_SIZE / WRITE_SIZE counters of the traffic
@@ -74,8 +79,12 @@ def main() -> int:
                     help="CPU-baseline sample budget (whole steps, at least one)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill",
-                                                                    "lin_prefill", "hbm_copy"])
+                                                                    "lin_prefill", "hbm_copy",
+                                                                    "gqa_decode", "lin_decode"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
+    ap.add_argument("--npast", type=int, default=4096, help="cached positions (gqa_decode)")
+    ap.add_argument("--rotate", type=int, default=0,
+                    help="bound layers cycled through (single-layer decode workloads)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -88,6 +97,8 @@ def main() -> int:
         return run_lin_prefill(args)
     if args.workload == "hbm_copy":
         return run_hbm_copy(args)
+    if args.workload in ("gqa_decode", "lin_decode"):
+        return run_layer_decode(args)
     return run_stack_decode(args)
 
 
@@ -433,6 +444,152 @@ def run_hbm_copy(args) -> int:
                          "traffic": None, "kernel": "torch elementwise mul (copy)",
                          "launches": K, "us_per_launch": round(us, 2)},
             "cpu_baseline": None}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_layer_decode(args) -> int:
+    """One decode call of one layer per unit of work, cycled over R bound
+    layers of the same kind inside one HIP graph; every call does the same
+    work (a GQA call at position n_past rewrites the same cache row)."""
+    import numpy as np
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip import synth as S
+    from ds4f_hip import workloads as W
+    from ds4f_hip.attn import GpuAttention, dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    gq, lg = W.GqaGeom(), W.LinGeom()
+    gqa = args.workload == "gqa_decode"
+    R = args.rotate or (128 if gqa else 256)
+    N, seed = args.npast, args.seed
+    pos = N if gqa else 3
+    ga = GpuAttention([2 if gqa else 1] * R, (N + 64) if gqa else 64, None)
+
+    def synth(n, dtype, dist, p0, p1, tid):
+        t = torch.empty(n, dtype=torch.float32 if dtype == 0 else torch.int16, device=dev)
+        L.check(lib.ds4f_hip_synth(dptr(t), n, dtype, dist, p0, p1, seed, tid, None), "synth")
+        return t
+
+    layers = []
+    for Lr in range(R):
+        d = {}
+        if gqa:
+            L.check(lib.ds4f_hip_synth_gqa_cache(Lr, N, seed, S.tid(S.GQA_KCACHE, Lr),
+                                                 S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
+            d["qn"] = synth(gq.head_dim, 1, 0, 1.0, 0.1, S.tid(S.GQA_QNW, Lr))
+            d["kn"] = synth(gq.head_dim, 1, 0, 1.0, 0.1, S.tid(S.GQA_KNW, Lr))
+            d["q"] = synth(gq.heads * 2 * gq.head_dim, 0, 0, 0.0, 1.0, S.tid(S.GQA_QGATE, Lr, N))
+            d["k"] = synth(gq.kv_heads * gq.head_dim, 0, 0, 0.0, 1.0, S.tid(S.GQA_K, Lr, N))
+            d["v"] = synth(gq.kv_heads * gq.head_dim, 0, 0, 0.0, 1.0, S.tid(S.GQA_V, Lr, N))
+            d["out"] = torch.empty(gq.heads * gq.head_dim, dtype=torch.float32, device=dev)
+        else:
+            L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr), None),
+                    "synth state")
+            L.check(lib.ds4f_hip_synth_conv_history(Lr, pos, seed, S.tid(S.LIN_CONVSTATE, Lr),
+                                                    None), "synth conv")
+            d["cw"] = synth(lg.rows * 4, 1, 0, 0.0, 0.1, S.tid(S.LIN_CONVW, Lr))
+            d["al"] = synth(lg.v_heads, 0, 1, 0.0, 2.7, S.tid(S.LIN_ALOG, Lr))
+            d["dt"] = synth(lg.v_heads, 1, 0, 0.0, 0.1, S.tid(S.LIN_DTB, Lr))
+            d["nw"] = synth(lg.vd, 1, 0, 1.0, 0.1, S.tid(S.LIN_NORMW, Lr))
+            d["qkv"] = synth(lg.rows, 0, 0, 0.0, 1.0, S.tid(S.LIN_QKV, Lr, 0))
+            d["z"] = synth(lg.v_heads * lg.vd, 0, 0, 0.0, 1.0, S.tid(S.LIN_Z, Lr, 0))
+            d["a"] = synth(lg.v_heads, 0, 0, 0.0, 1.0, S.tid(S.LIN_A, Lr, 0))
+            d["b"] = synth(lg.v_heads, 0, 0, 0.0, 1.0, S.tid(S.LIN_B, Lr, 0))
+            d["out"] = torch.empty(lg.v_heads * lg.vd, dtype=torch.float32, device=dev)
+        layers.append(d)
+    torch.cuda.synchronize()
+
+    def launch_all(stream):
+        for Lr, d in enumerate(layers):
+            if gqa:
+                rc = lib.ds4f_hip_gqa_decode_async(Lr, pos, dptr(d["q"]), dptr(d["k"]), dptr(d["v"]),
+                                                   dptr(d["qn"]), dptr(d["kn"]), dptr(d["out"]),
+                                                   None, stream)
+            else:
+                rc = lib.ds4f_hip_lin_decode_async(Lr, pos, dptr(d["qkv"]), dptr(d["z"]),
+                                                   dptr(d["a"]), dptr(d["b"]), dptr(d["cw"]),
+                                                   dptr(d["al"]), dptr(d["dt"]), dptr(d["nw"]),
+                                                   dptr(d["out"]), None, stream)
+            L.check(rc, f"layer {Lr}")
+
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        launch_all(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    reps = max(1, args.steps // R)
+    for _ in range(max(1, args.warmup // R)):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(reps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    calls = reps * R
+    us = ev0.elapsed_time(ev1) * 1e3 / calls
+    nbytes = gqa_layer_bytes(N) if gqa else LIN_LAYER_BYTES
+    gbps = nbytes / (us * 1e-6) / 1e9
+    kname = ("gqa decode = gqa_split_kernel + gqa_merge_kernel" if gqa else "lin_decode_kernel")
+    roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                "traffic": load_traffic(f"gqa_decode_ctx{N}" if gqa else "lin_decode"),
+                "kernel": kname, "launches": calls, "us_per_launch": round(us, 3),
+                "bytes_per_launch": nbytes}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        reps_cpu, secs = 0, 0.0
+        if gqa:
+            kc, vc = W.gqa_cache(gq, N, seed, 0)
+            half = gq.kv_heads * gq.head_dim
+            kv = np.zeros((N + 1, 2 * half), np.float32)
+            kv[:N, :half] = kc.reshape(N, half)
+            kv[:N, half:] = vc.reshape(N, half)
+            qn_h, kn_h = W.gqa_weights(gq, seed, 0)
+            q, k, v = W.gqa_token(gq, seed, 0, N)
+            while reps_cpu == 0 or secs < min(args.cpu_seconds, 5.0):
+                c0 = time.perf_counter()
+                O.gqa_body(kv, N, q.reshape(-1), k.reshape(-1).copy(), v.reshape(-1), qn_h, kn_h,
+                           gq.heads, gq.kv_heads, gq.head_dim)
+                secs += time.perf_counter() - c0
+                reps_cpu += 1
+        else:
+            wt = W.lin_weights(lg, seed, 0)
+            S0 = W.lin_state(lg, seed, 0).astype(np.float32)
+            ring = W.ring_from_history(lg, W.lin_conv_history(lg, seed, 0), pos)
+            qkv, z, a, b = W.lin_token(lg, seed, 0, 0)
+            while reps_cpu == 0 or secs < min(args.cpu_seconds, 5.0):
+                c0 = time.perf_counter()
+                O.lin_body(ring, S0, pos, qkv, z, a, b, wt.conv_w, wt.A_log, wt.dt_bias,
+                           wt.norm_w, lg.k_heads, lg.v_heads, lg.kd, lg.vd)
+                secs += time.perf_counter() - c0
+                reps_cpu += 1
+        cpu = {"value": round(reps_cpu / secs, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{reps_cpu} oracle {'gqa_body' if gqa else 'lin_body'} calls of the same "
+                         f"layer shape ({secs:.1f} s)"}
+    ga.close()
+    what = (f"GQA decode tokens/s (1 layer, 16q/2kv d256, n_past {N})" if gqa
+            else "gated delta-rule decode tokens/s (1 layer, 32 heads 128x128)")
+    line = {"metric": what, "value": round(1e6 / us, 1), "unit": "tokens/s", "n_gpus": 1,
+            "steps": calls, "warmup": max(1, args.warmup // R) * R, "ms_per_step": round(us / 1e3, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16-kv/fp32" if gqa else "f32",
+            "data": "synthetic (splitmix64 streams, seed 0)",
+            "config": {"workload": args.workload, "n_past": N if gqa else None, "position": pos,
+                       "layers_rotated": R,
+                       "rotated_state_bytes": R * (2048 * N if gqa else 2 * 1024 * 1024)},
+            "wall_ms_per_step": round(sec / calls * 1e3, 5),
+            "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
 
