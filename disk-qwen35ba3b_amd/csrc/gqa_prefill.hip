@@ -6,8 +6,10 @@
  * (src/attn_qwen.c:1222-1231): the results equal B decode steps in order.
  *
  * 1. prep:   one workgroup per new token: q_norm / k_norm + half-split RoPE
- *            (src/attn_qwen.c:287-326), the bf16 cache rows of k and v, and
- *            fp16 copies of q, k, v in MFMA-ready workspaces.
+ *            (src/attn_qwen.c:287-326), the bf16 cache rows of k, and fp16
+ *            copies of q and k in MFMA-ready workspaces; vprep: v into the
+ *            fp16 workspace and the bf16 cache, transposed through LDS per
+ *            32-key block.
  * 2. prefix: cache rows of positions before t0 (earlier chunks) into the
  *            fp16 key / value workspaces; zero padding rows (only launched
  *            when there are such rows).
@@ -58,6 +60,13 @@ __device__ __forceinline__ int v_slot(int r) {
     return ks * 16 + s16;
 }
 
+/* the inverse: key (0..31) held at slot s of a block */
+__device__ __forceinline__ int v_key(int s) {
+    const int ks = s >> 4, s16 = s & 15;
+    const int r16 = ((s16 >> 3) << 2) + (s16 & 3) + ((s16 & 4) ? 8 : 0);
+    return ks * 16 + r16;
+}
+
 __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
     const int b = blockIdx.x, pos = p.t0 + b;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, d0 = lane * 4;
@@ -73,18 +82,13 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
         rc = *reinterpret_cast<const float4 *>(rope + (d0 & (RD / 2 - 1)));
         rs = *reinterpret_cast<const float4 *>(rope + RD / 2 + (d0 & (RD / 2 - 1)));
     }
-    float4 xk[2], xv[2];
+    float4 xk[2];
     uint2 wk = make_uint2(0, 0);
     if (w == 0) {
         wk = *reinterpret_cast<const uint2 *>(p.kn_w + d0);
 #pragma unroll
         for (int g = 0; g < 2; g++)
             xk[g] = *reinterpret_cast<const float4 *>(p.k_in + ((size_t)b * p.kv_heads + g) * D + d0);
-    }
-    if (w == 1) {
-#pragma unroll
-        for (int g = 0; g < 2; g++)
-            xv[g] = *reinterpret_cast<const float4 *>(p.v_in + ((size_t)b * p.kv_heads + g) * D + d0);
     }
 
     const int qb = b >> 4, qp = b & 15;
@@ -113,17 +117,47 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
             for (int e = 0; e < 4; e++) p.kt[q35_k_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(yy[e]);
         }
     }
-    if (w == 1) {
-        const int slot = v_slot(kr);
+}
+
+/* v of the new tokens -> the fp16 value workspace and the bf16 cache,
+ * both dim-major ([dim][keys]).  One workgroup per (32-key block, kv head)
+ * transposes the block's rows through LDS, so consecutive lanes write
+ * consecutive keys of one dim row (64 B of workspace, 32 B of cache) rather
+ * than one 2-byte value per row.  Keys outside [t0, t0+B) are left alone:
+ * earlier positions belong to the cache, later ones are workspace padding. */
+__global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
+    const int kb = (p.t0 >> 5) + (int)blockIdx.x, g = blockIdx.y;
+    const int t = threadIdx.x;
+    __shared__ float sv[32][D + 1];
+    /* rows: key r of the block is position 32kb + r */
 #pragma unroll
-        for (int g = 0; g < 2; g++) {
-            const float vv[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+    for (int u = 0; u < 8; u++) {
+        const int idx = u * 256 + t, r = idx >> 6, c4 = (idx & 63) * 4;
+        const int pos = 32 * kb + r;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (pos >= p.t0 && pos < p.t0 + p.B)
+            v = *reinterpret_cast<const float4 *>(p.v_in + ((size_t)(pos - p.t0) * p.kv_heads + g) * D + c4);
+        sv[r][c4] = v.x;
+        sv[r][c4 + 1] = v.y;
+        sv[r][c4 + 2] = v.z;
+        sv[r][c4 + 3] = v.w;
+    }
+    q35_lds_barrier();
+    /* workspace: lane (d, slot) of 32 slots a dim row, key = the slot's key */
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                p.vw[(((size_t)g * p.kbt + kb) * D + d0 + e) * 32 + slot] = f16_bits(vv[e]);
-                p.vt[q35_v_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(vv[e]);
-            }
-        }
+    for (int u = 0; u < 32; u++) {
+        const int idx = u * 256 + t, d = idx >> 5, slot = idx & 31;
+        const int r = v_key(slot), pos = 32 * kb + r;
+        if (pos >= p.t0 && pos < p.t0 + p.B)
+            p.vw[(((size_t)g * p.kbt + kb) * D + d) * 32 + slot] = f16_bits(sv[r][d]);
+    }
+    /* cache: two 16-token tiles, lane (tile, d, token) */
+#pragma unroll
+    for (int u = 0; u < 32; u++) {
+        const int idx = u * 256 + t, tt = idx >> 12, d = (idx >> 4) & (D - 1), r16 = idx & 15;
+        const int r = tt * 16 + r16, pos = 32 * kb + r;
+        if (pos >= p.t0 && pos < p.t0 + p.B)
+            p.vt[q35_v_index(g, pos, d, p.t_tiles)] = q35_f2bf(sv[r][d]);
     }
 }
 
@@ -425,6 +459,12 @@ extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stre
     hipLaunchKernelGGL(prep_kernel, dim3(p.B), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    {
+        const int nvb = ((p.t0 + p.B - 1) >> 5) - (p.t0 >> 5) + 1;
+        hipLaunchKernelGGL(vprep_kernel, dim3(nvb, p.kv_heads), dim3(256), 0, stream, p);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     const int n_rows = p.t0 + (p.kbt * 32 - (p.t0 + p.B));    /* prefix + key padding */
     if (n_rows > 0) {
         const int64_t n = (int64_t)p.kv_heads * n_rows * D;
