@@ -131,8 +131,10 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     const int rows = 2 * KH * KD + VH * VD;
     const int b0 = c * C, nv = min(C, p.B - b0);
 
-    __shared__ __align__(16) float sK[C * XS];
-    __shared__ __align__(16) float sQA[C * XS];   /* Q, later A [C][AS] */
+    /* sK: K rows (later the V rows); sQA: Q rows, later A^T.  One buffer, so
+     * the output transpose at the end can use both halves. */
+    __shared__ __align__(16) float sbuf[2 * C * XS];
+    float *sK = sbuf, *sQA = sbuf + C * XS;
     __shared__ double sG[C];
     __shared__ float sBeta[C], sGq[C], sGk[C];
 
@@ -216,19 +218,46 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     }
     q35_lds_barrier();
 
+    /* Kd^T [kd][C] = exp(G_C - G_s) k_s[i]: thread (row i, keys 4q..4q+3)
+     * writes 16 contiguous bytes of a 256-byte row */
+    {
+        float *kdt = p.KdT + ((size_t)c * VH + h) * KD * C;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int idx = u * 256 + t, i = idx >> 4, s4 = (idx & 15) * 4;
+            float4 o;
+            o.x = sGk[s4 + 0] * sK[(s4 + 0) * XS + i];
+            o.y = sGk[s4 + 1] * sK[(s4 + 1) * XS + i];
+            o.z = sGk[s4 + 2] * sK[(s4 + 2) * XS + i];
+            o.w = sGk[s4 + 3] * sK[(s4 + 3) * XS + i];
+            *reinterpret_cast<float4 *>(kdt + (size_t)i * C + s4) = o;
+        }
+    }
+
     /* forward substitution, one right-hand-side column a thread:
      * columns 0..127 -> W (rhs beta_r exp(G_r) k_r), 128..255 -> U (beta_r v_r).
      * Right-looking: once x_s is final it is applied to every later row, so
      * each step is up to 63 independent FMAs (column s of A is row s of
-     * A^T, read four entries at a time). */
+     * A^T, read four entries at a time).  The W columns read K from LDS;
+     * the V rows then replace K there (16-byte loads) for the U columns. */
     float x[C];
     if (t < KD) {
 #pragma unroll
         for (int r = 0; r < C; r++) x[r] = sBeta[r] * sGq[r] * sK[r * XS + t];
-    } else {
-        const float *vcol = p.post + (size_t)b0 * rows + 2 * KH * KD + h * VD + (t - KD);
+    }
+    q35_lds_barrier();                     /* K no longer read */
 #pragma unroll
-        for (int r = 0; r < C; r++) x[r] = r < nv ? sBeta[r] * vcol[(size_t)r * rows] : 0.0f;
+    for (int u = 0; u < 8; u++) {
+        const int idx = u * 256 + t, r = idx >> 5, c4 = (idx & 31) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < nv)
+            v = *reinterpret_cast<const float4 *>(p.post + (size_t)(b0 + r) * rows + 2 * KH * KD + h * VD + c4);
+        *reinterpret_cast<float4 *>(&sK[r * XS + c4]) = v;
+    }
+    q35_lds_barrier();
+    if (t >= KD) {
+#pragma unroll
+        for (int r = 0; r < C; r++) x[r] = sBeta[r] * sK[r * XS + (t - KD)];
     }
 #pragma unroll
     for (int s = 0; s < C - 1; s++) {
@@ -241,17 +270,24 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
                 if (r4 + e > s) x[r4 + e] = fmaf(-el(a4, e), xs, x[r4 + e]);
         }
     }
-    float *dst = (t < KD ? p.W : p.U) + ((size_t)c * VH + h) * C * KD + (t & (KD - 1));
+    /* W and U rows out through LDS: [64 rows][256 columns (W | U)], then
+     * 16-byte row stores */
+    q35_lds_barrier();                     /* A^T and V no longer read */
+    constexpr int OSR = 2 * KD + 4;        /* output row stride (floats) */
 #pragma unroll
-    for (int r = 0; r < C; r++) dst[(size_t)r * KD] = x[r];
-
-    /* Kd^T [kd][C] = exp(G_C - G_s) k_s[i] */
+    for (int r = 0; r < C; r++) sbuf[r * OSR + t] = x[r];
+    q35_lds_barrier();
     {
-        float *kdt = p.KdT + ((size_t)c * VH + h) * KD * C;
-        const int s = t & 63;
-        const float f = sGk[s];
-#pragma unroll 8
-        for (int i = t >> 6; i < KD; i += 4) kdt[(size_t)i * C + s] = f * sK[s * XS + i];
+        float *wd = p.W + ((size_t)c * VH + h) * C * KD, *ud = p.U + ((size_t)c * VH + h) * C * VD;
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int idx = u * 256 + t, r = idx >> 6, c4 = (idx & 63) * 4;
+            const float4 o = *reinterpret_cast<const float4 *>(&sbuf[r * OSR + c4]);
+            if (c4 < KD)
+                *reinterpret_cast<float4 *>(wd + (size_t)r * KD + c4) = o;
+            else
+                *reinterpret_cast<float4 *>(ud + (size_t)r * VD + (c4 - KD)) = o;
+        }
     }
 }
 
