@@ -202,10 +202,6 @@ __global__ void qpad_kernel(Q35GqaPrefill p, int n_pad) {
 constexpr int KROW = 33, VROW = 5;
 constexpr int KTILE = 32 * KROW * 8, VTILE = D * VROW * 8;      /* halfs */
 
-/* dword 3 of a raw buffer resource on gfx9-family GPUs (no format
- * conversion, range checking against num_records) */
-constexpr int Q35_BUF_DW3 = 0x00020000;
-
 /* Instruction order for a block of 16 MFMAs fed by 16 LDS fragment reads:
  * 8 reads, then (4 MFMAs, 4 reads) x 3, then 4 MFMAs, so a batch of reads
  * is always in flight under the previous batch's MFMAs.  Left to itself
@@ -262,7 +258,6 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
     }
     const int kbase = (col * KROW + h) * 8;          /* + 16 ks halfs */
     const int vbase = (col * VROW + h) * 8;          /* + dt * 32 rows + 16 ks halfs */
-    typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
 
   for (int item = 0; item < 2; item++) {
     const int qb = item == 0 ? p.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;

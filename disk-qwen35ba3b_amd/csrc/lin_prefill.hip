@@ -292,162 +292,250 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
 }
 
 /* ---- 4. sequential scan over chunks per (value head, 16-column block) ---- *
- * 4 waves; wave w owns chunk rows 16w..16w+15 of Delta / O and key rows
- * 32w..32w+31 of the state block.  Workgroup n runs head
- * (n & 7) + 8 (n >> 6), block (n >> 3) & 7: the 8 blocks of a head share an
- * XCD (workgroups are dealt round-robin over the 8 XCDs), so the chunk
- * operands they all read stay in one L2.  The operands of chunk c+1 (they
- * do not depend on the state) are loaded into a second register set while
- * chunk c computes. */
-struct ScanOps {
-    float4 wa[8], qa[8], pa[4], ka[2][4];
-    float u[4], gq[4], gc;
+ * 8 waves in two roles.  Waves 0-3 compute from LDS only: wave w owns chunk
+ * rows 16w..16w+15 of Delta / O and key rows 32w..32w+31 of the state
+ * block.  Waves 4-7 move the chunk operands global -> registers -> LDS in
+ * two regions:
+ *   R1 = W, Q, the U slice and exp(G)   read in phase 1 (W S0, Q S0, Delta)
+ *   R2 = Pm, Kd^T and exp(G_C)          read in phase 2 (Pm Delta, S_end)
+ * R2 of chunk c is written while phase 1 of c runs, R1 of chunk c+1 while
+ * phase 2 of c runs, so each region is refilled under the other phase's
+ * MFMAs; a loader's global loads are issued one step before their data is
+ * written.  The compute waves issue no global loads inside the loop, so
+ * their output stores never make them wait, and the loaders' loads are
+ * unconditional, so their waits count exactly.
+ * Workgroup n runs head (n & 7) + 8 (n >> 6), block (n >> 3) & 7: the 8
+ * blocks of a head share an XCD (workgroups are dealt round-robin over the
+ * 8 XCDs), so the chunk operands they all read stay in one L2. */
+constexpr int OS = 20;                 /* LDS row stride of the U and O tiles */
+constexpr int SCAN_THREADS = 512;
+
+struct ScanLds {
+    float W[C * XS], Q[C * XS];        /* R1: rows [t][i] */
+    float U[C * OS];                   /* R1: [t][j] */
+    float Gq[C];                       /* R1: exp(G_t) */
+    float P[C * AS];                   /* R2: Pm [t][s], upper tiles zero */
+    float Kd[KD * AS];                 /* R2: Kd^T [i][s] */
+    float Gc[4];                       /* R2: exp(G_C) */
+    float S[16 * XS];                  /* state block [j][i] */
+    float D[16 * AS];                  /* Delta [j][t] */
+    float O[C * OS];                   /* O tile [t][j] */
 };
 
-struct ScanCtx {
-    int h, jb, kh, w, l16, lq, rows, VH;
+struct ScanGeo {
+    int h, jb, kh, VH, rows;
 };
 
-__device__ __forceinline__ void scan_load(ScanOps &o, const Q35LinPrefill &p, const ScanCtx &x,
-                                          int c) {
-    const int b0 = c * C, nv = min(C, p.B - b0);
-    const size_t ch = (size_t)c * x.VH + x.h;
-    const float *Wc = p.W + ch * C * KD, *Uc = p.U + ch * C * VD;
-    const float *Pc = p.Pm + ch * C * C, *Kc = p.KdT + ch * KD * C;
-    const float *gv = p.gvec + ch * Q35_LIN_GVEC;
-    const int row = 16 * x.w + x.l16;
-#pragma unroll
-    for (int blk = 0; blk < 8; blk++)
-        o.wa[blk] = *reinterpret_cast<const float4 *>(Wc + (size_t)row * KD + 16 * blk + 4 * x.lq);
-    /* every load is unconditional, so the compiler can count the loads in
-     * flight exactly and wait for this set only.  Rows past the batch read
-     * the last row's q: q row t only feeds output row t, which is not
-     * stored for those rows. */
-    const float *qrow = p.post + (size_t)(b0 + min(row, nv - 1)) * x.rows + x.kh * KD + 4 * x.lq;
-#pragma unroll
-    for (int blk = 0; blk < 8; blk++) o.qa[blk] = *reinterpret_cast<const float4 *>(qrow + 16 * blk);
-#pragma unroll
-    for (int blk = 0; blk < 4; blk++)   /* key blocks past the diagonal: unused */
-        o.pa[blk] = *reinterpret_cast<const float4 *>(Pc + (size_t)row * C + 16 * blk + 4 * x.lq);
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-        for (int blk = 0; blk < 4; blk++)
-            o.ka[tt][blk] = *reinterpret_cast<const float4 *>(
-                Kc + (size_t)(16 * (2 * x.w + tt) + x.l16) * C + 16 * blk + 4 * x.lq);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 16 * x.w + 4 * x.lq + i;
-        o.u[i] = Uc[(size_t)r * VD + 16 * x.jb + x.l16];
-        o.gq[i] = gv[r];
-    }
-    o.gc = gv[2 * C];
+/* Loader staging, lane lt of the 256 loader lanes.  All operand loads are
+ * raw buffer loads over the chunk's own block (range-checked, 32-bit lane
+ * offsets): W, Pm and Kd^T row group u of lane lt sits at byte
+ * 4096 u + 16 lt of its block. */
+struct StageR1 {
+    u32x4_t w[8], q[8], u, g;
+};
+struct StageR2 {
+    u32x4_t pm[4], kd[8], gc;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t blk_rsrc(const float *base, size_t n_floats) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, (int)(n_floats * 4), Q35_BUF_DW3);
 }
 
-__device__ __forceinline__ void scan_step(const ScanOps &o, const Q35LinPrefill &p,
-                                          const ScanCtx &x, int c, float *sS, float *sD) {
+__device__ __forceinline__ void r1_load(StageR1 &st, const Q35LinPrefill &p, const ScanGeo &g,
+                                        int c, int lt) {
     const int b0 = c * C, nv = min(C, p.B - b0);
-    const int w = x.w, l16 = x.l16, lq = x.lq;
-
-    /* W S0 and Q S0 (rows 16w.., all 128 key rows of the block) */
-    f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, aq = aw;
+    const size_t ch = (size_t)c * g.VH + g.h;
+    const __amdgpu_buffer_rsrc_t wr = blk_rsrc(p.W + ch * C * KD, C * KD);
+    const __amdgpu_buffer_rsrc_t qr = blk_rsrc(p.post + (size_t)b0 * g.rows, (size_t)nv * g.rows);
+    const __amdgpu_buffer_rsrc_t ur = blk_rsrc(p.U + ch * C * VD, C * VD);
+    const __amdgpu_buffer_rsrc_t gr = blk_rsrc(p.gvec + ch * Q35_LIN_GVEC, Q35_LIN_GVEC);
 #pragma unroll
-    for (int blk = 0; blk < 8; blk++) {
-        const float4 sb = *reinterpret_cast<const float4 *>(&sS[l16 * XS + 16 * blk + 4 * lq]);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            aw = mfma4(el(o.wa[blk], e), el(sb, e), aw);
-            aq = mfma4(el(o.qa[blk], e), el(sb, e), aq);
-        }
+    for (int u = 0; u < 8; u++) {
+        st.w[u] = __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lt, 4096 * u, 0);
+        /* rows past the batch read the last row's q: q row t only feeds
+         * output row t, which is not stored for those rows */
+        const int r = min(8 * u + (lt >> 5), nv - 1);
+        st.q[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, (r * g.rows + g.kh * KD + (lt & 31) * 4) * 4, 0, 0);
     }
-    float4 dl;
-    dl.x = o.u[0] - aw[0];
-    dl.y = o.u[1] - aw[1];
-    dl.z = o.u[2] - aw[2];
-    dl.w = o.u[3] - aw[3];
-    *reinterpret_cast<float4 *>(&sD[l16 * AS + 16 * w + 4 * lq]) = dl;
-    f32x4_t ao;
-#pragma unroll
-    for (int i = 0; i < 4; i++) ao[i] = o.gq[i] * aq[i];
-    q35_lds_barrier();
-
-    float4 db[4];
-#pragma unroll
-    for (int blk = 0; blk < 4; blk++)
-        db[blk] = *reinterpret_cast<const float4 *>(&sD[l16 * AS + 16 * blk + 4 * lq]);
-    /* O += Pm Delta (causal: key blocks 0..w) */
-#pragma unroll
-    for (int blk = 0; blk < 4; blk++) {
-        if (blk <= w) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) ao = mfma4(el(o.pa[blk], e), el(db[blk], e), ao);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 16 * w + 4 * lq + i;
-        if (r < nv) p.out[((size_t)(b0 + r) * x.VH + x.h) * VD + 16 * x.jb + l16] = ao[i];
-    }
-
-    /* S_end = exp(G_C) S0 + Kd^T Delta on key rows 32w..32w+31 */
-#pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        float *sp = &sS[l16 * XS + 16 * (2 * w + tt) + 4 * lq];
-        const float4 s0 = *reinterpret_cast<const float4 *>(sp);
-        f32x4_t acc = {o.gc * s0.x, o.gc * s0.y, o.gc * s0.z, o.gc * s0.w};
-#pragma unroll
-        for (int blk = 0; blk < 4; blk++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc = mfma4(el(o.ka[tt][blk], e), el(db[blk], e), acc);
-        *reinterpret_cast<float4 *>(sp) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    }
-    q35_lds_barrier();
+    st.u = __builtin_amdgcn_raw_buffer_load_b128(ur, ((lt >> 2) * VD + 16 * g.jb + (lt & 3) * 4) * 4, 0, 0);
+    st.g = __builtin_amdgcn_raw_buffer_load_b128(gr, 16 * (lt & 15), 0, 0);
 }
 
-__global__ __launch_bounds__(256) void scan_kernel(Q35LinPrefill p) {
+__device__ __forceinline__ void r1_store(const StageR1 &st, ScanLds &L, int lt) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int r = 8 * u + (lt >> 5), c4 = (lt & 31) * 4;
+        *reinterpret_cast<u32x4_t *>(&L.W[r * XS + c4]) = st.w[u];
+        *reinterpret_cast<u32x4_t *>(&L.Q[r * XS + c4]) = st.q[u];
+    }
+    *reinterpret_cast<u32x4_t *>(&L.U[(lt >> 2) * OS + (lt & 3) * 4]) = st.u;
+    /* lanes lt and lt + 16k write the same four values */
+    *reinterpret_cast<u32x4_t *>(&L.Gq[4 * (lt & 15)]) = st.g;
+}
+
+__device__ __forceinline__ void r2_load(StageR2 &st, const Q35LinPrefill &p, const ScanGeo &g,
+                                        int c, int lt) {
+    const size_t ch = (size_t)c * g.VH + g.h;
+    const __amdgpu_buffer_rsrc_t pr = blk_rsrc(p.Pm + ch * C * C, C * C);
+    const __amdgpu_buffer_rsrc_t kr = blk_rsrc(p.KdT + ch * KD * C, KD * C);
+    const __amdgpu_buffer_rsrc_t gr = blk_rsrc(p.gvec + ch * Q35_LIN_GVEC, Q35_LIN_GVEC);
+#pragma unroll
+    for (int u = 0; u < 4; u++) st.pm[u] = __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * lt, 4096 * u, 0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) st.kd[u] = __builtin_amdgcn_raw_buffer_load_b128(kr, 16 * lt, 4096 * u, 0);
+    st.gc = __builtin_amdgcn_raw_buffer_load_b128(gr, 2 * C * 4, 0, 0);
+}
+
+__device__ __forceinline__ void r2_store(const StageR2 &st, ScanLds &L, int lt) {
+    const int c4 = (lt & 15) * 4;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int r = 16 * u + (lt >> 4);
+        /* the chunk kernel leaves Pm's tiles above the diagonal unwritten */
+        const u32x4_t z = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4_t *>(&L.P[r * AS + c4]) = (c4 >> 4) > u ? z : st.pm[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+        *reinterpret_cast<u32x4_t *>(&L.Kd[(16 * u + (lt >> 4)) * AS + c4]) = st.kd[u];
+    *reinterpret_cast<u32x4_t *>(&L.Gc[0]) = st.gc;      /* all lanes: same value */
+}
+
+__global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     const int n = blockIdx.x;
-    ScanCtx x;
-    x.h = (n & 7) + 8 * (n >> 6);
-    x.jb = (n >> 3) & 7;
-    x.kh = x.h >> 1;
-    const int t = threadIdx.x, lane = t & 63;
-    x.w = t >> 6;
-    x.l16 = lane & 15;
-    x.lq = lane >> 4;
-    x.VH = p.v_heads;
-    x.rows = 2 * p.k_heads * KD + p.v_heads * VD;
+    ScanGeo g;
+    g.h = (n & 7) + 8 * (n >> 6);
+    g.jb = (n >> 3) & 7;
+    g.kh = g.h >> 1;
+    g.VH = p.v_heads;
+    g.rows = 2 * p.k_heads * KD + p.v_heads * VD;
+    const int t = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int last = p.n_chunks - 1;
 
-    __shared__ __align__(16) float sS[16 * XS];   /* state block, [j][i] */
-    __shared__ __align__(16) float sD[16 * AS];   /* Delta, [j][t] */
+    __shared__ __align__(16) ScanLds L;
+    float *state = p.state + ((size_t)g.h * VD + 16 * g.jb) * KD;
 
-    float *state = p.state + ((size_t)x.h * VD + 16 * x.jb) * KD;
+    if (wave >= 4) {
+        /* ---- loader waves ---- */
+        const int lt = t - 256;
+        StageR1 s1;
+        StageR2 s2;
+        r1_load(s1, p, g, 0, lt);
+        r2_load(s2, p, g, 0, lt);
+        r1_store(s1, L, lt);
+        r1_load(s1, p, g, min(1, last), lt);
+        q35_lds_barrier();                                   /* B0 */
+        /* the scheduling barriers keep each region's LDS writes ahead of
+         * the loads that refill its registers: issued in the other order,
+         * the loads go to fresh registers that must be copied back before
+         * the loop repeats, which waits for them */
+        for (int c = 0; c <= last; c++) {
+            /* phase 1 of c runs: R2 is free */
+            r2_store(s2, L, lt);
+            __builtin_amdgcn_sched_barrier(0);
+            r2_load(s2, p, g, min(c + 1, last), lt);
+            q35_lds_barrier();                               /* B1(c) */
+            /* phase 2 of c runs: R1 is free */
+            r1_store(s1, L, lt);
+            __builtin_amdgcn_sched_barrier(0);
+            r1_load(s1, p, g, min(c + 2, last), lt);
+            q35_lds_barrier();                               /* B2(c) */
+        }
+        return;
+    }
+
+    /* ---- compute waves ---- */
+    const int w = wave, lane = t & 63, l16 = lane & 15, lq = lane >> 4;
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int idx = u * 256 + t, j = idx >> 5, i4 = (idx & 31) * 4;
-        *reinterpret_cast<float4 *>(&sS[j * XS + i4]) =
+        *reinterpret_cast<float4 *>(&L.S[j * XS + i4]) =
             *reinterpret_cast<const float4 *>(state + (size_t)j * KD + i4);
     }
-    ScanOps A, B;
-    scan_load(A, p, x, 0);
-    q35_lds_barrier();
+    q35_lds_barrier();                                       /* B0 */
+    for (int c = 0; c <= last; c++) {
+        const int b0 = c * C, nv = min(C, p.B - b0);
 
-    /* the prefetch is unconditional (past the end it reloads the last chunk,
-     * unused): a conditional one would leave the compiler unable to count
-     * the loads in flight, and it would wait for all of them */
-    const int last = p.n_chunks - 1;
-    for (int c = 0; c < p.n_chunks; c += 2) {
-        scan_load(B, p, x, min(c + 1, last));
-        scan_step(A, p, x, c, sS, sD);
-        if (c + 1 > last) break;
-        scan_load(A, p, x, min(c + 2, last));
-        scan_step(B, p, x, c + 1, sS, sD);
+        /* phase 1: W S0 and Q S0 on rows 16w.. over all 128 key rows */
+        f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, aq = aw;
+#pragma unroll
+        for (int blk = 0; blk < 8; blk++) {
+            const int k = 16 * blk + 4 * lq;
+            const float4 sb = *reinterpret_cast<const float4 *>(&L.S[l16 * XS + k]);
+            const float4 wa = *reinterpret_cast<const float4 *>(&L.W[(16 * w + l16) * XS + k]);
+            const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[(16 * w + l16) * XS + k]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                aw = mfma4(el(wa, e), el(sb, e), aw);
+                aq = mfma4(el(qa, e), el(sb, e), aq);
+            }
+        }
+        f32x4_t ao;
+        float4 dl;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 16 * w + 4 * lq + i;
+            ao[i] = L.Gq[r] * aq[i];
+            const float d = L.U[r * OS + l16] - aw[i];
+            if (i == 0) dl.x = d;
+            if (i == 1) dl.y = d;
+            if (i == 2) dl.z = d;
+            if (i == 3) dl.w = d;
+        }
+        *reinterpret_cast<float4 *>(&L.D[l16 * AS + 16 * w + 4 * lq]) = dl;
+        q35_lds_barrier();                                   /* B1(c) */
+
+        /* phase 2: O += Pm Delta (key blocks 0..w), S_end on key rows 32w.. */
+        float4 db[4];
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++)
+            db[blk] = *reinterpret_cast<const float4 *>(&L.D[l16 * AS + 16 * blk + 4 * lq]);
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) {
+            if (blk <= w) {       /* w is wave-uniform: a scalar branch */
+                const float4 pa = *reinterpret_cast<const float4 *>(&L.P[(16 * w + l16) * AS + 16 * blk + 4 * lq]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) ao = mfma4(el(pa, e), el(db[blk], e), ao);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) L.O[(16 * w + 4 * lq + i) * OS + l16] = ao[i];
+        const float gc = L.Gc[0];
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            float *sp = &L.S[l16 * XS + 16 * (2 * w + tt) + 4 * lq];
+            const float4 s0 = *reinterpret_cast<const float4 *>(sp);
+            f32x4_t acc = {gc * s0.x, gc * s0.y, gc * s0.z, gc * s0.w};
+#pragma unroll
+            for (int blk = 0; blk < 4; blk++) {
+                const float4 ka = *reinterpret_cast<const float4 *>(
+                    &L.Kd[(16 * (2 * w + tt) + l16) * AS + 16 * blk + 4 * lq]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc = mfma4(el(ka, e), el(db[blk], e), acc);
+            }
+            *reinterpret_cast<float4 *>(sp) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        }
+        q35_lds_barrier();                                   /* B2(c) */
+
+        /* O rows of this chunk: one 16-byte store a lane, rows >= nv fall
+         * outside the buffer range and are dropped by the hardware */
+        {
+            const int r = t >> 2, c4 = (t & 3) * 4;
+            const float4 o = *reinterpret_cast<const float4 *>(&L.O[r * OS + c4]);
+            const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+                p.out + (size_t)b0 * g.VH * VD, 0, nv * g.VH * VD * 4, Q35_BUF_DW3);
+            const u32x4_t ov = {__float_as_uint(o.x), __float_as_uint(o.y), __float_as_uint(o.z),
+                                __float_as_uint(o.w)};
+            __builtin_amdgcn_raw_buffer_store_b128(ov, ors, ((r * g.VH + g.h) * VD + 16 * g.jb + c4) * 4, 0, 0);
+        }
     }
 
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int idx = u * 256 + t, j = idx >> 5, i4 = (idx & 31) * 4;
         *reinterpret_cast<float4 *>(state + (size_t)j * KD + i4) =
-            *reinterpret_cast<const float4 *>(&sS[j * XS + i4]);
+            *reinterpret_cast<const float4 *>(&L.S[j * XS + i4]);
     }
 }
 
@@ -504,7 +592,7 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(chunk_kernel, dim3(p.n_chunks, p.v_heads), dim3(256), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(SCAN_THREADS), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(gnorm_kernel, dim3(p.v_heads / 4, p.B), dim3(256), 0, stream, p);
     return hipGetLastError();

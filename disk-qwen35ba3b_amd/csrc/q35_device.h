@@ -11,6 +11,12 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+
+/* dword 3 of a raw buffer resource on gfx9-family GPUs (no format
+ * conversion, range checking against num_records: loads outside the range
+ * return zero, stores outside it are dropped) */
+constexpr int Q35_BUF_DW3 = 0x00020000;
 
 #define Q35_GQA_D 256       /* GQA head dim */
 #define Q35_GQA_GROUP 8     /* q heads per kv head */
