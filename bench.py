@@ -595,10 +595,13 @@ def run_layer_decode(args) -> int:
 
 
 def lin_prefill_flops(T: int, C: int = 64, heads: int = 32, dk: int = 128, dv: int = 128) -> float:
-    """Algorithmic flops of the chunked delta-rule prefill: per (value head,
-    chunk) 2C^2(3dk + 2dv) (K K^T, Q K^T, W, U, Pm Delta) + 6 C dk dv (W S,
-    Q S, Kd^T Delta) + 2C^3/3 (the triangular solve)."""
-    per = 2.0 * C * C * (3 * dk + 2 * dv) + 6.0 * C * dk * dv + 2.0 * C ** 3 / 3
+    """Algorithmic flops of the chunked delta-rule prefill, per (value head,
+    chunk): K K^T and Q K^T on their lower triangles, once per key head
+    (C^2 dk a value head); T = (I + A)^-1 (C^3 / 3); K S0, Q S0 and the
+    state update K^T Delta (6 C dk dv); T X and Pm Delta on their triangles
+    (2 C^2 dv).  Triangles are counted as C^2 / 2 entries, so the figure is
+    a lower bound on the work done."""
+    per = 1.0 * C * C * dk + C ** 3 / 3.0 + 6.0 * C * dk * dv + 2.0 * C * C * dv
     return per * heads * ((T + C - 1) // C)
 
 

@@ -497,10 +497,8 @@ int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const flo
     else
         CARVE(p.post, (size_t)B * P.rows);
     CARVE(p.gates, (size_t)B * vh * 2);
-    CARVE(p.W, nc * vh * 64 * P.kd);
-    CARVE(p.U, nc * vh * 64 * P.vd);
+    CARVE(p.T, nc * vh * 64 * 64);
     CARVE(p.Pm, nc * vh * 64 * 64);
-    CARVE(p.KdT, nc * vh * P.kd * 64);
     CARVE(p.gvec, nc * vh * Q35_LIN_GVEC);
 #undef CARVE
     HIPCHK(q35_lin_prefill(&p, pick(stream)));

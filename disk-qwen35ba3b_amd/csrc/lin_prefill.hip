@@ -11,26 +11,27 @@
  *   o_t = S^T q_t                                   (src/attn_qwen.c:666-690)
  * Over a chunk of C = 64 tokens with G_t = sum_{s<=t} g_s (from the chunk
  * start) and S0 the state entering the chunk, this unrolls exactly to
- *   A      = strict_lower( beta_t exp(G_t - G_s) k_t.k_s )
- *   W      = (I + A)^-1 diag(beta exp(G)) K       [C][kd]
- *   U      = (I + A)^-1 diag(beta) V              [C][vd]
- *   Delta  = U - W S0                             (the chunk's delta_t rows)
+ *   A      = strict_lower( beta_t exp(G_t - G_s) k_t.k_s ),  T = (I + A)^-1
+ *   Delta  = T diag(beta) (V - diag(exp(G)) K S0)   (the chunk's delta_t rows)
  *   O      = diag(exp(G)) Q S0 + Pm Delta,  Pm = lower( exp(G_t - G_s) q_t.k_s )
- *   S_end  = exp(G_C) S0 + Kd^T Delta,      Kd[s] = exp(G_C - G_s) k_s
- * Every factor exp(G_t - G_s) has s <= t, so none exceeds 1.
+ *   S_end  = exp(G_C) S0 + K^T diag(exp(G_C - G)) Delta
+ * (Delta is the WY form's U - W S0 with W = T diag(beta exp(G)) K and
+ * U = T diag(beta) V, applied without forming W and U.)  Every factor
+ * exp(G_t - G_s) has s <= t, so none exceeds 1.
  *
  * Kernels, in stream order:
  *   conv_kernel  per token: conv1d + SiLU (ring taps for positions before
  *                t0), q/k RMS-normalisation, gates -> post [B][rows] (the
  *                reference's mutated qkv) and gates [B][VH][2]
  *   ring_kernel  the last min(B, 4) raw rows into the conv ring
- *   chunk_kernel per (chunk, value head), all in parallel: K K^T and Q K^T
- *                on fp32 MFMA, A and Pm, the forward substitution that
- *                gives W and U, Kd^T and the decay vectors
+ *   chunk_kernel per (chunk, key head), all in parallel: K K^T and Q K^T
+ *                on fp32 MFMA (shared by the key head's two value heads),
+ *                then per value head A, Pm, the decay vectors and T by
+ *                forward substitution
  *   scan_kernel  per (value head, 16-column block of vd), sequential over
- *                chunks: the state block stays in LDS; Delta, O and S_end
- *                on fp32 MFMA (v_mfma_f32_16x16x4_f32); O unnormalised
- *                into out
+ *                chunks: the state block stays in LDS; K S0, Q S0, Delta,
+ *                O and S_end on fp32 MFMA (v_mfma_f32_16x16x4_f32); O
+ *                unnormalised into out
  *   gnorm_kernel per (token, value head): RMSNormGated of out with z
  *                (src/attn_qwen.c:726-749)
  * All arithmetic is fp32 (MFMA fp32 products are exact, accumulation fp32),
@@ -122,24 +123,29 @@ __global__ void ring_kernel(Q35LinPrefill p, int n) {
     p.ring[(size_t)(pos & 3) * rows + ch] = p.qkv[(size_t)b * rows + ch];
 }
 
-/* ---- 3. per (chunk, value head): A, Pm, W, U, Kd^T, decay vectors -------- */
+/* ---- 3. per (chunk, key head): decay vectors, Pm and T = (I + A)^-1 ------ *
+ * The two value heads 2kh, 2kh+1 of key head kh share K K^T and Q K^T; they
+ * differ in the gates.  Outputs per (chunk, value head): gvec, Pm (tiles on
+ * and below the diagonal) and T [64][64] (lower triangular, unit diagonal,
+ * zeros above). */
 __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
-    const int c = blockIdx.x, h = blockIdx.y, kh = h >> 1;
+    const int c = blockIdx.x, kh = blockIdx.y;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int l16 = lane & 15, lq = lane >> 4;
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
     const int b0 = c * C, nv = min(C, p.B - b0);
 
-    /* sK: K rows (later the V rows); sQA: Q rows, later A^T.  One buffer, so
-     * the output transpose at the end can use both halves. */
+    /* K and Q rows, later A^T of both value heads, later T of both */
     __shared__ __align__(16) float sbuf[2 * C * XS];
-    float *sK = sbuf, *sQA = sbuf + C * XS;
-    __shared__ double sG[C];
-    __shared__ float sBeta[C], sGq[C], sGk[C];
+    float *sK = sbuf, *sQ = sbuf + C * XS;
+    __shared__ double sG[2][C];
+    __shared__ float sBeta[2][C];
 
-    /* gates and the chunk-local cumulative log-decay (pads: g = beta = 0) */
-    if (w == 0) {
+    /* gates and the chunk-local cumulative log-decay of value head 2kh + w
+     * (pads: g = beta = 0) */
+    if (w < 2) {
+        const int h = 2 * kh + w;
         float g = 0.f, beta = 0.f;
         if (lane < nv) {
             const float2 gb = *reinterpret_cast<const float2 *>(p.gates + ((size_t)(b0 + lane) * VH + h) * 2);
@@ -152,18 +158,16 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
             const double o = __shfl_up(G, off);
             if (lane >= off) G += o;
         }
-        sG[lane] = G;
-        sBeta[lane] = beta;
+        sG[w][lane] = G;
+        sBeta[w][lane] = beta;
         const double Gc = __shfl(G, 63);
-        const float gq = (float)exp(G), gk = (float)exp(Gc - G);
-        sGq[lane] = gq;
-        sGk[lane] = gk;
         float *gv = p.gvec + ((size_t)c * VH + h) * Q35_LIN_GVEC;
-        gv[lane] = gq;
-        gv[C + lane] = gk;
-        if (lane == 0) gv[2 * C] = (float)exp(Gc);
+        gv[lane] = (float)exp(G);
+        gv[C + lane] = (float)exp(Gc - G);
+        gv[2 * C + lane] = beta;
+        if (lane == 0) gv[3 * C] = (float)exp(Gc);
     }
-    /* K and Q rows of the chunk (key head kh) into LDS; pad rows zero */
+    /* K and Q rows of the chunk into LDS; pad rows zero */
 #pragma unroll
     for (int u = 0; u < 8; u++) {
         const int idx = u * 256 + t, r = idx >> 5, c4 = (idx & 31) * 4;
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
             qv = *reinterpret_cast<const float4 *>(row + kh * KD + c4);
         }
         *reinterpret_cast<float4 *>(&sK[r * XS + c4]) = kv;
-        *reinterpret_cast<float4 *>(&sQA[r * XS + c4]) = qv;
+        *reinterpret_cast<float4 *>(&sQ[r * XS + c4]) = qv;
     }
     q35_lds_barrier();
 
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         const int n = w + 4 * k, m = n % 10;
         const int tr = m < 1 ? 0 : m < 3 ? 1 : m < 6 ? 2 : 3;
         const int tc = m - (tr * (tr + 1)) / 2;
-        const float *X = n < 10 ? sK : sQA;
+        const float *X = n < 10 ? sK : sQ;
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int blk = 0; blk < KD / 16; blk++) {
@@ -197,9 +201,12 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         }
         res[k] = acc;
     }
-    q35_lds_barrier();                       /* Q no longer read: its LDS becomes A^T */
-    float *sAT = sQA;
-    float *Pm = p.Pm + ((size_t)c * VH + h) * C * C;
+    q35_lds_barrier();                       /* K and Q no longer read */
+
+    /* A^T of value head v at sbuf + v C AS: A[r][s] = beta_r exp(G_r - G_s)
+     * k_r.k_s (s < r), stored [s][r];  Pm[r][s] = exp(G_r - G_s) q_r.k_s
+     * (s <= r) straight to its buffer */
+    float *sAT = sbuf;
 #pragma unroll
     for (int k = 0; k < 5; k++) {
         const int n = w + 4 * k, m = n % 10;
@@ -207,198 +214,195 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         const int tc = m - (tr * (tr + 1)) / 2;
         const int s = 16 * tc + l16;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 16 * tr + 4 * lq + i;
-            const float dec = expf((float)(sG[r] - sG[s]));
-            if (n < 10)
-                sAT[s * AS + r] = s < r ? sBeta[r] * dec * res[k][i] : 0.0f;
-            else
-                Pm[r * C + s] = s <= r ? dec * res[k][i] : 0.0f;
+        for (int v = 0; v < 2; v++) {
+            float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = 16 * tr + 4 * lq + i;
+                const float dec = expf((float)(sG[v][r] - sG[v][s]));
+                if (n < 10)
+                    sAT[v * C * AS + s * AS + r] = s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f;
+                else
+                    Pm[r * C + s] = s <= r ? dec * res[k][i] : 0.0f;
+            }
         }
     }
     q35_lds_barrier();
 
-    /* Kd^T [kd][C] = exp(G_C - G_s) k_s[i]: thread (row i, keys 4q..4q+3)
-     * writes 16 contiguous bytes of a 256-byte row */
-    {
-        float *kdt = p.KdT + ((size_t)c * VH + h) * KD * C;
+    /* T = (I + A)^-1 by forward substitution on the identity: waves 0 and 1
+     * (value heads 0 and 1), column j on lane j.  Right-looking: once x_s
+     * is final it is applied to every later row, so each step is up to 63
+     * independent FMAs (column s of A is row s of A^T, read four entries at
+     * a time, the same address across the wave). */
+    float x[C];
+    const int j = lane;
+    if (w < 2) {
+        const float *A = sAT + w * C * AS;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int idx = u * 256 + t, i = idx >> 4, s4 = (idx & 15) * 4;
-            float4 o;
-            o.x = sGk[s4 + 0] * sK[(s4 + 0) * XS + i];
-            o.y = sGk[s4 + 1] * sK[(s4 + 1) * XS + i];
-            o.z = sGk[s4 + 2] * sK[(s4 + 2) * XS + i];
-            o.w = sGk[s4 + 3] * sK[(s4 + 3) * XS + i];
-            *reinterpret_cast<float4 *>(kdt + (size_t)i * C + s4) = o;
+        for (int r = 0; r < C; r++) x[r] = r == j ? 1.0f : 0.0f;
+#pragma unroll
+        for (int s = 0; s < C - 1; s++) {
+            const float xs = x[s];
+#pragma unroll
+            for (int r4 = ((s + 1) >> 2) << 2; r4 < C; r4 += 4) {
+                const float4 a4 = *reinterpret_cast<const float4 *>(&A[s * AS + r4]);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (r4 + e > s) x[r4 + e] = fmaf(-el(a4, e), xs, x[r4 + e]);
+            }
         }
     }
-
-    /* forward substitution, one right-hand-side column a thread:
-     * columns 0..127 -> W (rhs beta_r exp(G_r) k_r), 128..255 -> U (beta_r v_r).
-     * Right-looking: once x_s is final it is applied to every later row, so
-     * each step is up to 63 independent FMAs (column s of A is row s of
-     * A^T, read four entries at a time).  The W columns read K from LDS;
-     * the V rows then replace K there (16-byte loads) for the U columns. */
-    float x[C];
-    if (t < KD) {
+    q35_lds_barrier();                       /* A^T no longer read */
+    if (w < 2) {
 #pragma unroll
-        for (int r = 0; r < C; r++) x[r] = sBeta[r] * sGq[r] * sK[r * XS + t];
+        for (int r = 0; r < C; r++) sbuf[w * C * AS + r * AS + j] = x[r];
     }
-    q35_lds_barrier();                     /* K no longer read */
+    q35_lds_barrier();
+    /* T rows out: 2 heads x 64 rows x 16 float4 */
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-        const int idx = u * 256 + t, r = idx >> 5, c4 = (idx & 31) * 4;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < nv)
-            v = *reinterpret_cast<const float4 *>(p.post + (size_t)(b0 + r) * rows + 2 * KH * KD + h * VD + c4);
-        *reinterpret_cast<float4 *>(&sK[r * XS + c4]) = v;
-    }
-    q35_lds_barrier();
-    if (t >= KD) {
-#pragma unroll
-        for (int r = 0; r < C; r++) x[r] = sBeta[r] * sK[r * XS + (t - KD)];
-    }
-#pragma unroll
-    for (int s = 0; s < C - 1; s++) {
-        const float xs = x[s];
-#pragma unroll
-        for (int r4 = ((s + 1) >> 2) << 2; r4 < C; r4 += 4) {
-            const float4 a4 = *reinterpret_cast<const float4 *>(&sAT[s * AS + r4]);
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (r4 + e > s) x[r4 + e] = fmaf(-el(a4, e), xs, x[r4 + e]);
-        }
-    }
-    /* W and U rows out through LDS: [64 rows][256 columns (W | U)], then
-     * 16-byte row stores */
-    q35_lds_barrier();                     /* A^T and V no longer read */
-    constexpr int OSR = 2 * KD + 4;        /* output row stride (floats) */
-#pragma unroll
-    for (int r = 0; r < C; r++) sbuf[r * OSR + t] = x[r];
-    q35_lds_barrier();
-    {
-        float *wd = p.W + ((size_t)c * VH + h) * C * KD, *ud = p.U + ((size_t)c * VH + h) * C * VD;
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int idx = u * 256 + t, r = idx >> 6, c4 = (idx & 63) * 4;
-            const float4 o = *reinterpret_cast<const float4 *>(&sbuf[r * OSR + c4]);
-            if (c4 < KD)
-                *reinterpret_cast<float4 *>(wd + (size_t)r * KD + c4) = o;
-            else
-                *reinterpret_cast<float4 *>(ud + (size_t)r * VD + (c4 - KD)) = o;
-        }
+        const int idx = u * 256 + t, v = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+        const float4 o = *reinterpret_cast<const float4 *>(&sbuf[v * C * AS + r * AS + c4]);
+        *reinterpret_cast<float4 *>(p.T + ((size_t)c * VH + 2 * kh + v) * C * C + r * C + c4) = o;
     }
 }
 
 /* ---- 4. sequential scan over chunks per (value head, 16-column block) ---- *
- * 8 waves in two roles.  Waves 0-3 compute from LDS only: wave w owns chunk
- * rows 16w..16w+15 of Delta / O and key rows 32w..32w+31 of the state
- * block.  Waves 4-7 move the chunk operands global -> registers -> LDS in
- * two regions:
- *   R1 = W, Q, the U slice and exp(G)   read in phase 1 (W S0, Q S0, Delta)
- *   R2 = Pm, Kd^T and exp(G_C)          read in phase 2 (Pm Delta, S_end)
- * R2 of chunk c is written while phase 1 of c runs, R1 of chunk c+1 while
- * phase 2 of c runs, so each region is refilled under the other phase's
- * MFMAs; a loader's global loads are issued one step before their data is
- * written.  The compute waves issue no global loads inside the loop, so
- * their output stores never make them wait, and the loaders' loads are
- * unconditional, so their waits count exactly.
- * Workgroup n runs head (n & 7) + 8 (n >> 6), block (n >> 3) & 7: the 8
- * blocks of a head share an XCD (workgroups are dealt round-robin over the
- * 8 XCDs), so the chunk operands they all read stay in one L2. */
-constexpr int OS = 20;                 /* LDS row stride of the U and O tiles */
+ * With S0 the state block entering the chunk (all 128 key rows, 16 value
+ * columns j), per chunk:
+ *   phase 1   K S0, Q S0;  X = diag(beta) (V - diag(exp(G)) K S0)
+ *   phase 1b  Delta = T X                       (= U - W S0)
+ *   phase 2   O = diag(exp(G)) Q S0 + Pm Delta
+ *             S_end = exp(G_C) S0 + K^T diag(exp(G_C - G)) Delta
+ * 8 waves in two roles.  Waves 0-3 compute from LDS only: wave w owns rows
+ * 16w.. of X and Delta, rows 16(3-w).. of O (so the causal products are
+ * balanced: 116 MFMAs a wave), and key rows 32w..32w+31 of the state
+ * block.  Waves 4-7 move the operands global -> registers -> LDS:
+ *   R1 = Q, the V slice, exp(G), beta   read in phase 1,  refilled in 1b
+ *   R2 = T, Pm, exp(G_C - G), exp(G_C)  read in 1b and 2, refilled in 1
+ *   K (double-buffered)                 read in 1 and 2,  refilled in 2
+ * so each refill runs under other phases' MFMAs; a loader's global loads
+ * are issued one step before their data is written.  The compute waves
+ * issue no global loads inside the loop, so their output stores never make
+ * them wait, and the loaders' loads are unconditional raw buffer loads
+ * (range-checked: rows past the batch read as zero), so their waits count
+ * exactly.  Workgroup n runs head (n & 7) + 8 (n >> 6), block (n >> 3) & 7:
+ * the 8 blocks of a head share an XCD (workgroups are dealt round-robin
+ * over the 8 XCDs), so the operands they all read stay in one L2. */
+constexpr int OS = 20;                 /* LDS row stride of the V tile */
 constexpr int SCAN_THREADS = 512;
 
 struct ScanLds {
-    float W[C * XS], Q[C * XS];        /* R1: rows [t][i] */
-    float U[C * OS];                   /* R1: [t][j] */
-    float Gq[C];                       /* R1: exp(G_t) */
+    float K[2][C * XS];                /* K rows [t][i], chunk c in K[c & 1] */
+    float Q[C * XS];                   /* R1: Q rows [t][i] */
+    float V[C * OS];                   /* R1: V slice [t][j] */
+    float Gq[C], Beta[C];              /* R1 */
+    float T[C * AS];                   /* R2: T [t][s] */
     float P[C * AS];                   /* R2: Pm [t][s], upper tiles zero */
-    float Kd[KD * AS];                 /* R2: Kd^T [i][s] */
+    float Gk[C];                       /* R2: exp(G_C - G_s) */
     float Gc[4];                       /* R2: exp(G_C) */
     float S[16 * XS];                  /* state block [j][i] */
+    float X[16 * AS];                  /* X [j][t] */
     float D[16 * AS];                  /* Delta [j][t] */
-    float O[C * OS];                   /* O tile [t][j] */
 };
 
 struct ScanGeo {
-    int h, jb, kh, VH, rows;
+    int h, jb, kh, VH, KH, rows;
 };
 
 /* Loader staging, lane lt of the 256 loader lanes.  All operand loads are
- * raw buffer loads over the chunk's own block (range-checked, 32-bit lane
- * offsets): W, Pm and Kd^T row group u of lane lt sits at byte
- * 4096 u + 16 lt of its block. */
+ * raw buffer loads over the chunk's own block with 32-bit lane offsets; T
+ * and Pm row group u of lane lt sits at byte 4096 u + 16 lt of its block. */
 struct StageR1 {
-    u32x4_t w[8], q[8], u, g;
+    u32x4_t q[8], v, gq, beta;
 };
 struct StageR2 {
-    u32x4_t pm[4], kd[8], gc;
+    u32x4_t t[4], pm[4], gk, gc;
+};
+struct StageK {
+    u32x4_t k[8];
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t blk_rsrc(const float *base, size_t n_floats) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, (int)(n_floats * 4), Q35_BUF_DW3);
 }
 
+/* the post rows of chunk c (rows at and past the batch end read as zero) */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t post_rsrc(const Q35LinPrefill &p, const ScanGeo &g, int c) {
+    const int b0 = c * C, nv = min(C, p.B - b0);
+    return blk_rsrc(p.post + (size_t)b0 * g.rows, (size_t)nv * g.rows);
+}
+
 __device__ __forceinline__ void r1_load(StageR1 &st, const Q35LinPrefill &p, const ScanGeo &g,
                                         int c, int lt) {
-    const int b0 = c * C, nv = min(C, p.B - b0);
     const size_t ch = (size_t)c * g.VH + g.h;
-    const __amdgpu_buffer_rsrc_t wr = blk_rsrc(p.W + ch * C * KD, C * KD);
-    const __amdgpu_buffer_rsrc_t qr = blk_rsrc(p.post + (size_t)b0 * g.rows, (size_t)nv * g.rows);
-    const __amdgpu_buffer_rsrc_t ur = blk_rsrc(p.U + ch * C * VD, C * VD);
+    const __amdgpu_buffer_rsrc_t qr = post_rsrc(p, g, c);
     const __amdgpu_buffer_rsrc_t gr = blk_rsrc(p.gvec + ch * Q35_LIN_GVEC, Q35_LIN_GVEC);
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-        st.w[u] = __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lt, 4096 * u, 0);
-        /* rows past the batch read the last row's q: q row t only feeds
-         * output row t, which is not stored for those rows */
-        const int r = min(8 * u + (lt >> 5), nv - 1);
+        const int r = 8 * u + (lt >> 5);
         st.q[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, (r * g.rows + g.kh * KD + (lt & 31) * 4) * 4, 0, 0);
     }
-    st.u = __builtin_amdgcn_raw_buffer_load_b128(ur, ((lt >> 2) * VD + 16 * g.jb + (lt & 3) * 4) * 4, 0, 0);
-    st.g = __builtin_amdgcn_raw_buffer_load_b128(gr, 16 * (lt & 15), 0, 0);
+    st.v = __builtin_amdgcn_raw_buffer_load_b128(
+        qr, ((lt >> 2) * g.rows + 2 * g.KH * KD + g.h * VD + 16 * g.jb + (lt & 3) * 4) * 4, 0, 0);
+    st.gq = __builtin_amdgcn_raw_buffer_load_b128(gr, 16 * (lt & 15), 0, 0);
+    st.beta = __builtin_amdgcn_raw_buffer_load_b128(gr, (2 * C + 4 * (lt & 15)) * 4, 0, 0);
 }
 
 __device__ __forceinline__ void r1_store(const StageR1 &st, ScanLds &L, int lt) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int r = 8 * u + (lt >> 5), c4 = (lt & 31) * 4;
-        *reinterpret_cast<u32x4_t *>(&L.W[r * XS + c4]) = st.w[u];
-        *reinterpret_cast<u32x4_t *>(&L.Q[r * XS + c4]) = st.q[u];
-    }
-    *reinterpret_cast<u32x4_t *>(&L.U[(lt >> 2) * OS + (lt & 3) * 4]) = st.u;
+    for (int u = 0; u < 8; u++)
+        *reinterpret_cast<u32x4_t *>(&L.Q[(8 * u + (lt >> 5)) * XS + (lt & 31) * 4]) = st.q[u];
+    *reinterpret_cast<u32x4_t *>(&L.V[(lt >> 2) * OS + (lt & 3) * 4]) = st.v;
     /* lanes lt and lt + 16k write the same four values */
-    *reinterpret_cast<u32x4_t *>(&L.Gq[4 * (lt & 15)]) = st.g;
+    *reinterpret_cast<u32x4_t *>(&L.Gq[4 * (lt & 15)]) = st.gq;
+    *reinterpret_cast<u32x4_t *>(&L.Beta[4 * (lt & 15)]) = st.beta;
+}
+
+__device__ __forceinline__ void k_load(StageK &st, const Q35LinPrefill &p, const ScanGeo &g, int c,
+                                       int lt) {
+    const __amdgpu_buffer_rsrc_t kr = post_rsrc(p, g, c);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int r = 8 * u + (lt >> 5);
+        st.k[u] = __builtin_amdgcn_raw_buffer_load_b128(
+            kr, (r * g.rows + (g.KH + g.kh) * KD + (lt & 31) * 4) * 4, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void k_store(const StageK &st, float *Kb, int lt) {
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+        *reinterpret_cast<u32x4_t *>(&Kb[(8 * u + (lt >> 5)) * XS + (lt & 31) * 4]) = st.k[u];
 }
 
 __device__ __forceinline__ void r2_load(StageR2 &st, const Q35LinPrefill &p, const ScanGeo &g,
                                         int c, int lt) {
     const size_t ch = (size_t)c * g.VH + g.h;
+    const __amdgpu_buffer_rsrc_t tr = blk_rsrc(p.T + ch * C * C, C * C);
     const __amdgpu_buffer_rsrc_t pr = blk_rsrc(p.Pm + ch * C * C, C * C);
-    const __amdgpu_buffer_rsrc_t kr = blk_rsrc(p.KdT + ch * KD * C, KD * C);
     const __amdgpu_buffer_rsrc_t gr = blk_rsrc(p.gvec + ch * Q35_LIN_GVEC, Q35_LIN_GVEC);
 #pragma unroll
-    for (int u = 0; u < 4; u++) st.pm[u] = __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * lt, 4096 * u, 0);
-#pragma unroll
-    for (int u = 0; u < 8; u++) st.kd[u] = __builtin_amdgcn_raw_buffer_load_b128(kr, 16 * lt, 4096 * u, 0);
-    st.gc = __builtin_amdgcn_raw_buffer_load_b128(gr, 2 * C * 4, 0, 0);
+    for (int u = 0; u < 4; u++) {
+        st.t[u] = __builtin_amdgcn_raw_buffer_load_b128(tr, 16 * lt, 4096 * u, 0);
+        st.pm[u] = __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * lt, 4096 * u, 0);
+    }
+    st.gk = __builtin_amdgcn_raw_buffer_load_b128(gr, (C + 4 * (lt & 15)) * 4, 0, 0);
+    st.gc = __builtin_amdgcn_raw_buffer_load_b128(gr, 3 * C * 4, 0, 0);
 }
 
 __device__ __forceinline__ void r2_store(const StageR2 &st, ScanLds &L, int lt) {
     const int c4 = (lt & 15) * 4;
+    const u32x4_t z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int r = 16 * u + (lt >> 4);
+        *reinterpret_cast<u32x4_t *>(&L.T[r * AS + c4]) = st.t[u];
         /* the chunk kernel leaves Pm's tiles above the diagonal unwritten */
-        const u32x4_t z = {0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4_t *>(&L.P[r * AS + c4]) = (c4 >> 4) > u ? z : st.pm[u];
     }
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-        *reinterpret_cast<u32x4_t *>(&L.Kd[(16 * u + (lt >> 4)) * AS + c4]) = st.kd[u];
-    *reinterpret_cast<u32x4_t *>(&L.Gc[0]) = st.gc;      /* all lanes: same value */
+    *reinterpret_cast<u32x4_t *>(&L.Gk[4 * (lt & 15)]) = st.gk;   /* lanes lt, lt + 16k: same values */
+    *reinterpret_cast<u32x4_t *>(&L.Gc[0]) = st.gc;               /* all lanes: same value */
 }
 
 __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
@@ -408,6 +412,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     g.jb = (n >> 3) & 7;
     g.kh = g.h >> 1;
     g.VH = p.v_heads;
+    g.KH = p.k_heads;
     g.rows = 2 * p.k_heads * KD + p.v_heads * VD;
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -421,121 +426,146 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
         const int lt = t - 256;
         StageR1 s1;
         StageR2 s2;
+        StageK sk;
         r1_load(s1, p, g, 0, lt);
+        k_load(sk, p, g, 0, lt);
         r2_load(s2, p, g, 0, lt);
         r1_store(s1, L, lt);
+        k_store(sk, L.K[0], lt);
+        __builtin_amdgcn_sched_barrier(0);
         r1_load(s1, p, g, min(1, last), lt);
+        k_load(sk, p, g, min(1, last), lt);
         q35_lds_barrier();                                   /* B0 */
-        /* the scheduling barriers keep each region's LDS writes ahead of
-         * the loads that refill its registers: issued in the other order,
-         * the loads go to fresh registers that must be copied back before
-         * the loop repeats, which waits for them */
+        /* the scheduling barriers keep each set's LDS writes ahead of the
+         * loads that refill its registers: issued in the other order, the
+         * loads go to fresh registers that must be copied back before the
+         * loop repeats, which waits for them */
         for (int c = 0; c <= last; c++) {
             /* phase 1 of c runs: R2 is free */
             r2_store(s2, L, lt);
             __builtin_amdgcn_sched_barrier(0);
             r2_load(s2, p, g, min(c + 1, last), lt);
             q35_lds_barrier();                               /* B1(c) */
-            /* phase 2 of c runs: R1 is free */
+            /* phase 1b of c runs: R1 is free */
             r1_store(s1, L, lt);
             __builtin_amdgcn_sched_barrier(0);
             r1_load(s1, p, g, min(c + 2, last), lt);
             q35_lds_barrier();                               /* B2(c) */
+            /* phase 2 of c runs: K[(c + 1) & 1] is free */
+            k_store(sk, L.K[(c + 1) & 1], lt);
+            __builtin_amdgcn_sched_barrier(0);
+            k_load(sk, p, g, min(c + 2, last), lt);
+            q35_lds_barrier();                               /* B3(c) */
         }
         return;
     }
 
     /* ---- compute waves ---- */
     const int w = wave, lane = t & 63, l16 = lane & 15, lq = lane >> 4;
+    const int rx = 16 * w, ro = 16 * (3 - w);        /* X / Delta rows, O rows */
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-        const int idx = u * 256 + t, j = idx >> 5, i4 = (idx & 31) * 4;
-        *reinterpret_cast<float4 *>(&L.S[j * XS + i4]) =
-            *reinterpret_cast<const float4 *>(state + (size_t)j * KD + i4);
+        const int idx = u * 256 + t, jj = idx >> 5, i4 = (idx & 31) * 4;
+        *reinterpret_cast<float4 *>(&L.S[jj * XS + i4]) =
+            *reinterpret_cast<const float4 *>(state + (size_t)jj * KD + i4);
     }
     q35_lds_barrier();                                       /* B0 */
     for (int c = 0; c <= last; c++) {
         const int b0 = c * C, nv = min(C, p.B - b0);
+        const float *Kc = L.K[c & 1];
 
-        /* phase 1: W S0 and Q S0 on rows 16w.. over all 128 key rows */
-        f32x4_t aw = {0.f, 0.f, 0.f, 0.f}, aq = aw;
+        /* phase 1: K S0 on rows rx, Q S0 on rows ro, over all 128 key rows */
+        f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, aq = ak;
 #pragma unroll
         for (int blk = 0; blk < 8; blk++) {
             const int k = 16 * blk + 4 * lq;
             const float4 sb = *reinterpret_cast<const float4 *>(&L.S[l16 * XS + k]);
-            const float4 wa = *reinterpret_cast<const float4 *>(&L.W[(16 * w + l16) * XS + k]);
-            const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[(16 * w + l16) * XS + k]);
+            const float4 ka = *reinterpret_cast<const float4 *>(&Kc[(rx + l16) * XS + k]);
+            const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[(ro + l16) * XS + k]);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                aw = mfma4(el(wa, e), el(sb, e), aw);
+                ak = mfma4(el(ka, e), el(sb, e), ak);
                 aq = mfma4(el(qa, e), el(sb, e), aq);
             }
         }
         f32x4_t ao;
-        float4 dl;
+        float xr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int r = 16 * w + 4 * lq + i;
-            ao[i] = L.Gq[r] * aq[i];
-            const float d = L.U[r * OS + l16] - aw[i];
-            if (i == 0) dl.x = d;
-            if (i == 1) dl.y = d;
-            if (i == 2) dl.z = d;
-            if (i == 3) dl.w = d;
+            const int r = rx + 4 * lq + i;
+            xr[i] = L.Beta[r] * (L.V[r * OS + l16] - L.Gq[r] * ak[i]);
+            ao[i] = L.Gq[ro + 4 * lq + i] * aq[i];
         }
-        *reinterpret_cast<float4 *>(&L.D[l16 * AS + 16 * w + 4 * lq]) = dl;
+        *reinterpret_cast<float4 *>(&L.X[l16 * AS + rx + 4 * lq]) = make_float4(xr[0], xr[1], xr[2], xr[3]);
         q35_lds_barrier();                                   /* B1(c) */
 
-        /* phase 2: O += Pm Delta (key blocks 0..w), S_end on key rows 32w.. */
+        /* phase 1b: Delta = T X on rows rx (key blocks 0..w) */
+        f32x4_t ad = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) {
+            if (blk <= w) {       /* w is wave-uniform: a scalar branch */
+                const float4 ta = *reinterpret_cast<const float4 *>(&L.T[(rx + l16) * AS + 16 * blk + 4 * lq]);
+                const float4 xb = *reinterpret_cast<const float4 *>(&L.X[l16 * AS + 16 * blk + 4 * lq]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) ad = mfma4(el(ta, e), el(xb, e), ad);
+            }
+        }
+        *reinterpret_cast<float4 *>(&L.D[l16 * AS + rx + 4 * lq]) = make_float4(ad[0], ad[1], ad[2], ad[3]);
+        q35_lds_barrier();                                   /* B2(c) */
+
+        /* phase 2: O += Pm Delta on rows ro (key blocks 0..3-w) */
         float4 db[4];
 #pragma unroll
         for (int blk = 0; blk < 4; blk++)
             db[blk] = *reinterpret_cast<const float4 *>(&L.D[l16 * AS + 16 * blk + 4 * lq]);
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
-            if (blk <= w) {       /* w is wave-uniform: a scalar branch */
-                const float4 pa = *reinterpret_cast<const float4 *>(&L.P[(16 * w + l16) * AS + 16 * blk + 4 * lq]);
+            if (blk <= 3 - w) {
+                const float4 pa = *reinterpret_cast<const float4 *>(&L.P[(ro + l16) * AS + 16 * blk + 4 * lq]);
 #pragma unroll
                 for (int e = 0; e < 4; e++) ao = mfma4(el(pa, e), el(db[blk], e), ao);
             }
         }
+        {
+            /* rows >= nv fall outside the buffer range: the hardware drops them */
+            const __amdgpu_buffer_rsrc_t ors = blk_rsrc(p.out + (size_t)b0 * g.VH * VD, (size_t)nv * g.VH * VD);
 #pragma unroll
-        for (int i = 0; i < 4; i++) L.O[(16 * w + 4 * lq + i) * OS + l16] = ao[i];
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __float_as_uint(ao[i]), ors, (((ro + 4 * lq + i) * g.VH + g.h) * VD + 16 * g.jb + l16) * 4, 0, 0);
+        }
+        /* S_end on key rows 32w..32w+31: A = K^T (one LDS dword per lane
+         * and MFMA), B = exp(G_C - G_s) Delta */
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) {
+            const float4 gk = *reinterpret_cast<const float4 *>(&L.Gk[16 * blk + 4 * lq]);
+            db[blk].x *= gk.x;
+            db[blk].y *= gk.y;
+            db[blk].z *= gk.z;
+            db[blk].w *= gk.w;
+        }
         const float gc = L.Gc[0];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
-            float *sp = &L.S[l16 * XS + 16 * (2 * w + tt) + 4 * lq];
+            const int i0 = 16 * (2 * w + tt);
+            float *sp = &L.S[l16 * XS + i0 + 4 * lq];
             const float4 s0 = *reinterpret_cast<const float4 *>(sp);
             f32x4_t acc = {gc * s0.x, gc * s0.y, gc * s0.z, gc * s0.w};
 #pragma unroll
-            for (int blk = 0; blk < 4; blk++) {
-                const float4 ka = *reinterpret_cast<const float4 *>(
-                    &L.Kd[(16 * (2 * w + tt) + l16) * AS + 16 * blk + 4 * lq]);
+            for (int blk = 0; blk < 4; blk++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc = mfma4(el(ka, e), el(db[blk], e), acc);
-            }
+                for (int e = 0; e < 4; e++)
+                    acc = mfma4(Kc[(16 * blk + 4 * lq + e) * XS + i0 + l16], el(db[blk], e), acc);
             *reinterpret_cast<float4 *>(sp) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         }
-        q35_lds_barrier();                                   /* B2(c) */
-
-        /* O rows of this chunk: one 16-byte store a lane, rows >= nv fall
-         * outside the buffer range and are dropped by the hardware */
-        {
-            const int r = t >> 2, c4 = (t & 3) * 4;
-            const float4 o = *reinterpret_cast<const float4 *>(&L.O[r * OS + c4]);
-            const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
-                p.out + (size_t)b0 * g.VH * VD, 0, nv * g.VH * VD * 4, Q35_BUF_DW3);
-            const u32x4_t ov = {__float_as_uint(o.x), __float_as_uint(o.y), __float_as_uint(o.z),
-                                __float_as_uint(o.w)};
-            __builtin_amdgcn_raw_buffer_store_b128(ov, ors, ((r * g.VH + g.h) * VD + 16 * g.jb + c4) * 4, 0, 0);
-        }
+        q35_lds_barrier();                                   /* B3(c) */
     }
 
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-        const int idx = u * 256 + t, j = idx >> 5, i4 = (idx & 31) * 4;
-        *reinterpret_cast<float4 *>(state + (size_t)j * KD + i4) =
-            *reinterpret_cast<const float4 *>(&L.S[j * XS + i4]);
+        const int idx = u * 256 + t, jj = idx >> 5, i4 = (idx & 31) * 4;
+        *reinterpret_cast<float4 *>(state + (size_t)jj * KD + i4) =
+            *reinterpret_cast<const float4 *>(&L.S[jj * XS + i4]);
     }
 }
 
@@ -571,11 +601,9 @@ extern "C" void q35_lin_prefill_ws_bytes(int B, int k_heads, int v_heads, int wi
     size_t n = 0;
     if (with_post) n += (size_t)B * rows;                       /* post */
     n += (size_t)B * vh * 2;                                    /* gates */
-    n += nc * vh * C * KD * 2;                                  /* W, U */
-    n += nc * vh * C * C;                                       /* Pm */
-    n += nc * vh * KD * C;                                      /* KdT */
+    n += nc * vh * C * C * 2;                                   /* T, Pm */
     n += nc * vh * Q35_LIN_GVEC;                                /* gvec */
-    *bytes = n * sizeof(float) + 8 * 256;     /* + alignment of the 7 pieces */
+    *bytes = n * sizeof(float) + 6 * 256;     /* + alignment of the 5 pieces */
 }
 
 extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stream) {
@@ -590,7 +618,7 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     const int nr = p.B < 4 ? p.B : 4;
     hipLaunchKernelGGL(ring_kernel, grid_for((int64_t)nr * rows, 256), dim3(256), 0, stream, p, nr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(chunk_kernel, dim3(p.n_chunks, p.v_heads), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(chunk_kernel, dim3(p.n_chunks, p.k_heads), dim3(256), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(SCAN_THREADS), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -43,8 +43,8 @@ hipError_t q35_lin_decode(const Q35LinDecode *p, hipStream_t stream);
  *   post  [B][rows]          post-conv, normed q | k | v (the caller's
  *                            qkv_post, or a workspace)
  *   gates [B][VH][2]         (log-decay g, beta)
- *   W, U  [nc][VH][64][128]  Pm [nc][VH][64][64]  KdT [nc][VH][128][64]
- *   gvec  [nc][VH][Q35_LIN_GVEC]  exp(G_t), exp(G_C - G_t), exp(G_C) */
+ *   T, Pm [nc][VH][64][64]   (I + A)^-1 and the masked decayed Q K^T
+ *   gvec  [nc][VH][Q35_LIN_GVEC]  exp(G_t) | exp(G_C - G_t) | beta_t | exp(G_C) */
 #define Q35_LIN_GVEC 256
 typedef struct Q35LinPrefill {
     const float *qkv, *z, *a, *b;  /* [B][rows], [B][VH*VD], [B][VH], [B][VH] */
@@ -53,7 +53,7 @@ typedef struct Q35LinPrefill {
     float *ring;                   /* [4][rows] */
     float *state;                  /* [vh][vd][kd] */
     float *out;                    /* [B][VH*VD] */
-    float *post, *gates, *W, *U, *Pm, *KdT, *gvec;
+    float *post, *gates, *T, *Pm, *gvec;
     int t0, B, n_chunks, k_heads, v_heads;
 } Q35LinPrefill;
 /* workspace bytes, post included when with_post != 0 */
