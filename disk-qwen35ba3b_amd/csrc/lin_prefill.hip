@@ -23,11 +23,11 @@
  *   conv_kernel  per token: conv1d + SiLU (ring taps for positions before
  *                t0), q/k RMS-normalisation, gates -> post [B][rows] (the
  *                reference's mutated qkv) and gates [B][VH][2]
- *   ring_kernel  the last min(B, 4) raw rows into the conv ring
  *   chunk_kernel per (chunk, key head), all in parallel: K K^T and Q K^T
  *                on fp32 MFMA (shared by the key head's two value heads),
  *                then per value head A, Pm, the decay vectors and T by
- *                forward substitution
+ *                forward substitution; the last chunk's workgroups also
+ *                write the last min(B, 4) raw rows into the conv ring
  *   scan_kernel  per (value head, 16-column block of vd), sequential over
  *                chunks: the state block stays in LDS; K S0, Q S0, Delta,
  *                O and S_end on fp32 MFMA (v_mfma_f32_16x16x4_f32); O
@@ -55,54 +55,67 @@ __device__ __forceinline__ float el(const float4 &v, int e) {
 }
 
 /* ---- 1. conv + SiLU, q/k norms, gates ------------------------------------ *
- * grid (rows / 512, ceil(B / 8)), 4 waves; wave w owns 128-channel group
- * 4*blockIdx.x + w (q heads, then k heads, then v heads), 2 channels a
- * lane, for 8 consecutive tokens: the 11 raw rows they tap are loaded once
- * (a sliding window instead of 4 loads per output). */
-constexpr int CT = 8;
+ * grid (rows / 1024, ceil(B / 16)), 4 waves; wave w owns channels
+ * 256 (4 blockIdx.x + w) .. +255, two 128-channel head groups (q heads,
+ * then k heads, then v heads), one per half-wave, 4 channels a lane, for
+ * 16 consecutive tokens: the 19 raw rows they tap are loaded once (a
+ * sliding window instead of 4 loads per output).  The q / k norm of a
+ * head is a half-wave sum.  Against the reference's per-element IEEE
+ * divisions, the SiLU uses v_exp_f32 / v_rcp_f32 and the norm one
+ * reciprocal per token (each about 1 ulp): the kernel then runs at the
+ * HBM rate of its 2 x B x rows x 4 bytes. */
+constexpr int CT = 16;
 __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
     const int bb = blockIdx.y * CT;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
-    const int grp = 4 * blockIdx.x + w;
-    const int c0 = grp * 128 + 2 * lane;
+    const int c0 = (4 * blockIdx.x + w) * 256 + 4 * lane;
+    const int grp = c0 >> 7;                       /* 128-channel group */
+    /* k_heads is even, so both groups of a wave are q, both k or both v */
+    const bool normed = grp < 2 * KH;
 
     /* raw rows of positions t0+bb-3 .. t0+bb+CT-1 */
-    float2 xr[CT + 3];
+    float4 xr[CT + 3];
 #pragma unroll
     for (int k = 0; k < CT + 3; k++) {
         const int b = bb - 3 + k, pp = p.t0 + b;
-        float2 v = make_float2(0.f, 0.f);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (b >= 0 && b < p.B)
-            v = *reinterpret_cast<const float2 *>(p.qkv + (size_t)b * rows + c0);
+            v = *reinterpret_cast<const float4 *>(p.qkv + (size_t)b * rows + c0);
         else if (b < 0 && pp >= 0)
-            v = *reinterpret_cast<const float2 *>(p.ring + (size_t)(pp & 3) * rows + c0);
+            v = *reinterpret_cast<const float4 *>(p.ring + (size_t)(pp & 3) * rows + c0);
         xr[k] = v;
     }
-    const uint4 wv = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4);
+    const uint4 wa = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4);
+    const uint4 wb = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4 + 8);
+    const uint2 wt[4] = {make_uint2(wa.x, wa.y), make_uint2(wa.z, wa.w), make_uint2(wb.x, wb.y),
+                         make_uint2(wb.z, wb.w)};
+    const float scale = grp < KH ? 1.0f / (float)KD : 1.0f / sqrtf((float)KD);
 #pragma unroll
     for (int j = 0; j < CT; j++) {
         const int b = bb + j, pos = p.t0 + b;
         if (b >= p.B) break;
-        const float x0[4] = {xr[j].x, xr[j + 1].x, xr[j + 2].x, xr[j + 3].x};
-        const float x1[4] = {xr[j].y, xr[j + 1].y, xr[j + 2].y, xr[j + 3].y};
-        float y0 = q35_conv_silu(x0, make_uint2(wv.x, wv.y), pos);
-        float y1 = q35_conv_silu(x1, make_uint2(wv.z, wv.w), pos);
-        if (grp < 2 * KH) {        /* q or k head: RMS norm (src/attn_qwen.c:522-538) */
-#pragma clang fp contract(off)
-            double ss = (double)y0 * y0 + (double)y1 * y1;
-            ss = q35_wave_sum(ss);
-            const float r = sqrtf((float)(ss / (double)KD) + 1e-6f);
-            const float scale = grp < KH ? 1.0f / (float)KD : 1.0f / sqrtf((float)KD);
-            y0 = y0 / r * scale;
-            y1 = y1 / r * scale;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float x[4] = {el(xr[j], e), el(xr[j + 1], e), el(xr[j + 2], e), el(xr[j + 3], e)};
+            y[e] = q35_conv_silu_fast(x, wt[e], pos);
         }
-        *reinterpret_cast<float2 *>(p.post + (size_t)b * rows + c0) = make_float2(y0, y1);
+        if (normed) {              /* q or k head: RMS norm (src/attn_qwen.c:522-538) */
+#pragma clang fp contract(off)
+            double ss = (double)y[0] * y[0] + (double)y[1] * y[1] + (double)y[2] * y[2] + (double)y[3] * y[3];
+            ss = q35_half_sum(ss);
+            const float r = sqrtf((float)(ss / (double)KD) + 1e-6f), ri = 1.0f / r;
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = y[e] * ri * scale;
+        }
+        *reinterpret_cast<float4 *>(p.post + (size_t)b * rows + c0) = make_float4(y[0], y[1], y[2], y[3]);
     }
 
-    if (blockIdx.x == 0) {
-        for (int i = threadIdx.x; i < CT * VH; i += 256) {
+    /* gates of the block's tokens, spread over the row-group workgroups */
+    {
+        for (int i = threadIdx.x * gridDim.x + blockIdx.x; i < CT * VH; i += 256 * gridDim.x) {
             const int b = bb + i / VH, h = i % VH;
             if (b >= p.B) break;
             float g, beta;
@@ -111,16 +124,6 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
             *reinterpret_cast<float2 *>(p.gates + ((size_t)b * VH + h) * 2) = make_float2(g, beta);
         }
     }
-}
-
-/* ---- 2. ring: slot pos%4 <- raw row of pos, for the last min(B, 4) tokens */
-__global__ void ring_kernel(Q35LinPrefill p, int n) {
-    const int rows = 2 * p.k_heads * KD + p.v_heads * VD;
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)n * rows) return;
-    const int r = (int)(i / rows), ch = (int)(i % rows);
-    const int b = p.B - n + r, pos = p.t0 + b;
-    p.ring[(size_t)(pos & 3) * rows + ch] = p.qkv[(size_t)b * rows + ch];
 }
 
 /* ---- 3. per (chunk, key head): decay vectors, Pm and T = (I + A)^-1 ------ *
@@ -135,6 +138,18 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
     const int b0 = c * C, nv = min(C, p.B - b0);
+
+    /* the conv ring: slot pos % 4 <- raw row of pos for the last min(B, 4)
+     * tokens, written by the last chunk's workgroups (the conv kernel, which
+     * reads the ring, has finished) */
+    if (c == p.n_chunks - 1) {
+        const int nr = min(p.B, 4), n4 = rows / 4;
+        for (int i = kh * 256 + t; i < nr * n4; i += KH * 256) {
+            const int b = p.B - nr + i / n4, c4 = 4 * (i % n4);
+            *reinterpret_cast<float4 *>(p.ring + (size_t)((p.t0 + b) & 3) * rows + c4) =
+                *reinterpret_cast<const float4 *>(p.qkv + (size_t)b * rows + c4);
+        }
+    }
 
     /* K and Q rows, later A^T of both value heads, later T of both */
     __shared__ __align__(16) float sbuf[2 * C * XS];
@@ -590,7 +605,6 @@ __global__ __launch_bounds__(256) void gnorm_kernel(Q35LinPrefill p) {
     *reinterpret_cast<float2 *>(p.out + off) = y;
 }
 
-inline dim3 grid_for(int64_t n, int bs) { return dim3((unsigned)((n + bs - 1) / bs)); }
 
 }  // namespace
 
@@ -610,14 +624,11 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     const Q35LinPrefill &p = *pin;
     const int rows = 2 * p.k_heads * KD + p.v_heads * VD;
     if (p.B < 1 || p.t0 < 0 || p.v_heads != 2 * p.k_heads || p.v_heads % 8 != 0 ||
-        rows % 512 != 0 || p.n_chunks != (p.B + C - 1) / C)
+        p.k_heads % 2 != 0 || rows % 1024 != 0 || p.n_chunks != (p.B + C - 1) / C)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(conv_kernel, dim3(rows / 512, (p.B + CT - 1) / CT), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(conv_kernel, dim3(rows / 1024, (p.B + CT - 1) / CT), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int nr = p.B < 4 ? p.B : 4;
-    hipLaunchKernelGGL(ring_kernel, grid_for((int64_t)nr * rows, 256), dim3(256), 0, stream, p, nr);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(chunk_kernel, dim3(p.n_chunks, p.k_heads), dim3(256), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(SCAN_THREADS), 0, stream, p);

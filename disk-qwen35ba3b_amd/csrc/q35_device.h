@@ -88,6 +88,17 @@ __device__ __forceinline__ T q35_wave_sum(T v) {
     return (q35_readlane(v, 0) + q35_readlane(v, 16)) + (q35_readlane(v, 32) + q35_readlane(v, 48));
 }
 
+/* sum over each 32-lane half of a wave, the half's total in each of its
+ * lanes (all 64 lanes must be active) */
+template <typename T>
+__device__ __forceinline__ T q35_half_sum(T v) {
+    v = q35_sum8(v);
+    v += q35_dpp<0x140>(v);
+    const T lo = q35_readlane(v, 0) + q35_readlane(v, 16);
+    const T hi = q35_readlane(v, 32) + q35_readlane(v, 48);
+    return (threadIdx.x & 32) ? hi : lo;
+}
+
 /* Workgroup barrier that orders LDS only.  __syncthreads() carries a
  * workgroup-scope fence over all address spaces, which gfx950 implements as
  * s_waitcnt vmcnt(0) lgkmcnt(0) before s_barrier: every global load in
@@ -179,6 +190,20 @@ __device__ __forceinline__ float q35_conv_silu(const float (&x)[4], uint2 w, int
     for (int k = 0; k < 4; k++)
         if (pos - 3 + k >= 0) acc += x[k] * q35_bf2f(wt[k]);
     return acc * q35_sigmoid(acc);
+}
+
+/* The same with exp and the reciprocal on the hardware's approximate
+ * instructions (v_exp_f32 of x log2(e), v_rcp_f32: about 1 ulp each for
+ * the conv outputs' range); for the throughput-bound prefill. */
+__device__ __forceinline__ float q35_conv_silu_fast(const float (&x)[4], uint2 w, int pos) {
+#pragma clang fp contract(off)
+    const uint16_t wt[4] = {(uint16_t)(w.x & 0xffff), (uint16_t)(w.x >> 16),
+                            (uint16_t)(w.y & 0xffff), (uint16_t)(w.y >> 16)};
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (pos - 3 + k >= 0) acc += x[k] * q35_bf2f(wt[k]);
+    return acc * __builtin_amdgcn_rcpf(1.0f + __expf(-acc));
 }
 
 /* Delta-rule gates of one value head (src/attn_qwen.c:545-551, :664-665):
