@@ -6,9 +6,10 @@
  * k_norm, half-split partial RoPE, cache write of the new k / v, softmax
  * attention of 16 q heads over 2 kv heads, sigmoid output gate.
  *
- * Kernel 1 (split): grid = (P chunks, kv heads), 256 threads.  A workgroup
- * streams `chunk` cached positions of one kv head and serves all 8 q heads
- * of that kv head from the same K/V bytes:
+ * Kernel 1 (split): grid = (P chunks, kv heads), 512 threads (8 waves, one
+ * q head's norm / RoPE each).  A workgroup streams `chunk` cached positions
+ * of one kv head and serves all 8 q heads of that kv head from the same K/V
+ * bytes; wave w takes the 16-position tiles w, w + 8, ...:
  *   scores  S[16 pos][16 col] = K[16 pos][256] * Q^T on 16x16x32 bf16 MFMA,
  *           columns 0-7 holding the bf16 "hi" part of the 8 q heads and
  *           columns 8-15 the "lo" remainder (q = hi + lo to ~2^-16), so the
@@ -16,7 +17,7 @@
  *           one DPP lane exchange;
  *   values  O^T[16 dim][16 col] += V^T[16 dim][16 pos] * P^T on 16x16x16
  *           bf16 MFMA, P split the same way (hi | lo columns);
- *   online softmax per wave, the 4 waves merged in LDS, one partial
+ *   online softmax per wave, the 8 waves merged in LDS, one partial
  *   (max, sum, O[8][256]) written per workgroup.
  * The new token (position `token`) is attended in fp32 from registers (as
  * the reference does with its fp32 cache) by the last chunk's workgroup,
@@ -33,35 +34,35 @@
 namespace {
 
 constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
-constexpr int NT = 256, NW = 4;
+#ifndef Q35_GQA_NW
+#define Q35_GQA_NW 8        /* waves per workgroup */
+#endif
+constexpr int NW = Q35_GQA_NW, NT = 64 * NW;
+constexpr int HPW = G / NW;           /* q heads normed per wave in the prologue */
 constexpr int MAX_CHUNKS = 256;
 constexpr int OS = 9;                 /* sO row stride (8 heads + 1): conflict-free */
 constexpr float SCALE = 0.0625f;      /* 1/sqrtf(256), src/attn_qwen.c:334 */
-#ifndef Q35_GQA_PIPE
-#define Q35_GQA_PIPE 1      /* register buffers per wave (1 or 2) */
-#endif
-#ifndef Q35_GQA_MINW
-#define Q35_GQA_MINW 2      /* waves per SIMD the register budget targets */
-#endif
-
 struct KTile { bf16x8_t k[8]; };
 struct VTile { s16x4_t v[16]; };
 
-__device__ __forceinline__ void load_k(KTile &kt, const uint16_t *base, int lane) {
-    /* base: the 16-token tile's first 16x32 block; block kk at +kk*512 */
-    const int m = lane & 15, grp = lane >> 4;
+/* Tile loads are raw buffer loads over the workgroup's own chunk: `off` is
+ * the tile's byte offset (8192 bytes a tile) plus the lane's; a tile past
+ * the chunk's end lies outside the resource's range, and the hardware
+ * returns zeros for it without a memory access.  Nontemporal: the KV is
+ * streamed once, and the delta-rule states stay cache-resident. */
+__device__ __forceinline__ void load_k(KTile &kt, __amdgpu_buffer_rsrc_t rs, int off) {
+    /* lane: block kk at +kk*1024 bytes, row lane & 15 (+64 B), 8 dims at
+     * (lane >> 4) * 16 B */
 #pragma unroll
     for (int kk = 0; kk < 8; kk++)
-        kt.k[kk] = __builtin_nontemporal_load(
-            reinterpret_cast<const bf16x8_t *>(base + kk * 512 + m * 32 + grp * 8));
+        kt.k[kk] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + kk * 1024, 0, 2));
 }
-__device__ __forceinline__ void load_v(VTile &vt, const uint16_t *base, int lane) {
-    /* base: the tile's [256 dim][16 tok] block; dims 16dt.. at +dt*256 */
-    const int m = lane & 15, grp = lane >> 4;
+__device__ __forceinline__ void load_v(VTile &vt, __amdgpu_buffer_rsrc_t rs, int off) {
+    /* lane: dim row 16dt + (lane & 15) (+32 B a row), 4 tokens at
+     * (lane >> 4) * 8 B; dim block dt at +dt*512 bytes */
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
-        vt.v[dt] = __builtin_nontemporal_load(
-            reinterpret_cast<const s16x4_t *>(base + (dt * 16 + m) * 16 + grp * 4));
+        vt.v[dt] = __builtin_bit_cast(s16x4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, off + dt * 512, 0, 2));
 }
 
 /* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
@@ -118,8 +119,7 @@ __device__ __forceinline__ void attend_tile(const KTile &kt, VTile &vt, const bf
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt.v[dt], pb, acc[dt], 0, 0, 0);
 }
 
-template <int PIPE, int MINW>
-__global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
+__global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     const int c = blockIdx.x, g = blockIdx.y;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int n_past = p.token;
@@ -128,6 +128,20 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
     const bool last = (c == p.n_chunks - 1);
     const int d0 = lane * 4;
 
+    /* this wave's first K/V tile is requested right after the prologue's
+     * own loads (loads complete in issue order, so the prologue's waits do
+     * not cover it), and its HBM latency runs under the q norm / RoPE work */
+    const int n_sub = (c1 > c0) ? (c1 - c0 + 15) >> 4 : 0;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(p.kt + (size_t)g * p.t_tiles * (D / 32) * 512 +
+                                                (size_t)(c0 >> 4) * (D / 32) * 512)),
+        0, n_sub * 8192, Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(p.vt + (size_t)g * p.t_tiles * D * 16 + (size_t)(c0 >> 4) * D * 16)),
+        0, n_sub * 8192, Q35_BUF_DW3);
+    const int wv = __builtin_amdgcn_readfirstlane(w);
+    const int koff = (lane & 15) * 64 + (lane >> 4) * 16, voff = (lane & 15) * 32 + (lane >> 4) * 8;
+
     __shared__ float sQ[G][D];
     __shared__ bf16x8_t sQb[8 * 64];
     __shared__ float sO[NW][D * OS];
@@ -135,10 +149,10 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
     __shared__ float sKn[D], sVn[D];
 
     /* ---- prologue: every input in flight at once ---- */
-    float4 xq[2];
+    float4 xq[HPW];
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++)
-        xq[hh] = *reinterpret_cast<const float4 *>(p.q_gate + (size_t)(g * G + 2 * w + hh) * 2 * D +
+    for (int hh = 0; hh < HPW; hh++)
+        xq[hh] = *reinterpret_cast<const float4 *>(p.q_gate + (size_t)(g * G + HPW * w + hh) * 2 * D +
                                                    d0);
     const uint2 wq = *reinterpret_cast<const uint2 *>(p.qn_w + d0);
     float4 rc = make_float4(1.f, 1.f, 1.f, 1.f), rs = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -154,15 +168,19 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
         xv = *reinterpret_cast<const float4 *>(p.v_new + (size_t)g * D + d0);
         wk = *reinterpret_cast<const uint2 *>(p.kn_w + d0);
     }
+    KTile ka;
+    VTile va;
+    load_k(ka, krs, wv * 8192 + koff);
+    load_v(va, vrs, wv * 8192 + voff);
 
-    /* q of heads 2w, 2w+1 (of this kv head): norm + RoPE, then straight into
+    /* q of heads HPW*w .. HPW*w+HPW-1 (of this kv head): norm + RoPE, then straight into
      * the MFMA B-operand layout: entry [kk][lane'] holds 8 bf16 of column
      * n = lane'&15 (head n&7, hi if n<8 else lo) for dims 32kk + 8*(lane'>>4).
      * This lane's dims 4l..4l+3 are half of one such entry. */
     const int kk0 = d0 >> 5, gp0 = (d0 >> 3) & 3, half = (d0 >> 2) & 1;
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const int qh = 2 * w + hh;
+    for (int hh = 0; hh < HPW; hh++) {
+        const int qh = HPW * w + hh;
         const float4 y = q35_norm_rope_head(xq[hh], wq, rc, rs, lane);
         *reinterpret_cast<float4 *>(&sQ[qh][d0]) = y;
         const float yy[4] = {y.x, y.y, y.z, y.w};
@@ -202,40 +220,15 @@ __global__ __launch_bounds__(NT, MINW) void gqa_split_kernel(Q35GqaDecode p) {
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int n_sub = (c1 > c0) ? (c1 - c0 + 15) >> 4 : 0;
-    const uint16_t *kbase = p.kt + (size_t)g * p.t_tiles * (D / 32) * 512 +
-                            (size_t)(c0 >> 4) * (D / 32) * 512;
-    const uint16_t *vbase = p.vt + (size_t)g * p.t_tiles * D * 16 + (size_t)(c0 >> 4) * D * 16;
-    const int n_mine = (n_sub > w) ? (n_sub - w + NW - 1) / NW : 0;
-    KTile ka, kb;
-    VTile va, vb;
-    if (PIPE == 1) {
-        for (int i = 0; i < n_mine; i++) {
-            const int s0 = w + i * NW;
-            load_k(ka, kbase + (size_t)s0 * (D / 32) * 512, lane);
-            load_v(va, vbase + (size_t)s0 * D * 16, lane);
-            attend_tile(ka, va, sQb, lane, c0 + 16 * s0, c1, grp, is_lo, m_run, l_run, acc);
-        }
-    } else {
-        if (n_mine > 0) {
-            load_k(ka, kbase + (size_t)w * (D / 32) * 512, lane);
-            load_v(va, vbase + (size_t)w * D * 16, lane);
-        }
-        for (int i = 0; i < n_mine; i += 2) {
-            const int s0 = w + i * NW, s1 = s0 + NW;
-            if (i + 1 < n_mine) {
-                load_k(kb, kbase + (size_t)s1 * (D / 32) * 512, lane);
-                load_v(vb, vbase + (size_t)s1 * D * 16, lane);
-            }
-            attend_tile(ka, va, sQb, lane, c0 + 16 * s0, c1, grp, is_lo, m_run, l_run, acc);
-            if (i + 1 < n_mine) {
-                if (i + 2 < n_mine) {
-                    load_k(ka, kbase + (size_t)(s1 + NW) * (D / 32) * 512, lane);
-                    load_v(va, vbase + (size_t)(s1 + NW) * D * 16, lane);
-                }
-                attend_tile(kb, vb, sQb, lane, c0 + 16 * s1, c1, grp, is_lo, m_run, l_run, acc);
-            }
-        }
+    /* tiles wv, wv + NW, ...: each one's loads are issued (unconditionally;
+     * past the chunk they read zeros at no cost) as soon as the previous
+     * tile has been consumed */
+    const int n_mine = (n_sub > wv) ? (n_sub - wv + NW - 1) / NW : 0;
+    for (int i = 0; i < n_mine; i++) {
+        const int s0 = wv + i * NW;
+        attend_tile(ka, va, sQb, lane, c0 + 16 * s0, c1, grp, is_lo, m_run, l_run, acc);
+        load_k(ka, krs, (s0 + NW) * 8192 + koff);
+        load_v(va, vrs, (s0 + NW) * 8192 + voff);
     }
 
     /* ---- per-wave partial: l over the 4 lane groups; O hi + lo columns ---- */
@@ -370,7 +363,7 @@ extern "C" int q35_gqa_max_chunks(void) { return MAX_CHUNKS; }
 extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) {
     if (p->heads != p->kv_heads * G || p->n_chunks < 1 || p->n_chunks > MAX_CHUNKS)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gqa_split_kernel<Q35_GQA_PIPE, Q35_GQA_MINW>), dim3(p->n_chunks, p->kv_heads),
+    hipLaunchKernelGGL(gqa_split_kernel, dim3(p->n_chunks, p->kv_heads),
                        dim3(NT), 0, stream, *p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

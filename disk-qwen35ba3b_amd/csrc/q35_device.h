@@ -13,6 +13,18 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
 
+/* A pointer every lane holds the same value of, moved to scalar registers.
+ * A buffer resource must be uniform; built from an address the compiler
+ * computed in vector registers (64-bit products are VALU work on gfx9), it
+ * would be wrapped in a readfirstlane loop at every load. */
+template <typename T>
+__device__ __forceinline__ T *q35_uniform_ptr(T *ptr) {
+    const uint64_t v = (uint64_t)ptr;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+
 /* dword 3 of a raw buffer resource on gfx9-family GPUs (no format
  * conversion, range checking against num_records: loads outside the range
  * return zero, stores outside it are dropped) */
