@@ -126,6 +126,11 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
     }
 }
 
+/* 16x16 blocks of a 64x64 triangle: index of block (a, c), a <= c, among the
+ * 10 blocks on and above the diagonal */
+__device__ __forceinline__ int blk_q(int a, int c) { return a * (9 - a) / 2 + (c - a); }
+constexpr int BS = 20, BLK = 16 * BS;
+
 /* ---- 3. per (chunk, key head): decay vectors, Pm and T = (I + A)^-1 ------ *
  * The two value heads 2kh, 2kh+1 of key head kh share K K^T and Q K^T; they
  * differ in the gates.  Outputs per (chunk, value head): gvec, Pm (tiles on
@@ -133,7 +138,7 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
  * zeros above). */
 __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     const int c = blockIdx.x, kh = blockIdx.y;
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     const int l16 = lane & 15, lq = lane >> 4;
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
@@ -218,10 +223,19 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     }
     q35_lds_barrier();                       /* K and Q no longer read */
 
-    /* A^T of value head v at sbuf + v C AS: A[r][s] = beta_r exp(G_r - G_s)
-     * k_r.k_s (s < r), stored [s][r];  Pm[r][s] = exp(G_r - G_s) q_r.k_s
-     * (s <= r) straight to its buffer */
-    float *sAT = sbuf;
+    /* T = (I + A)^-1 in 16x16 blocks.  With M = A^T (strictly upper,
+     * M[s][r] = A[r][s]) and U = (I + M)^-1 = T^T, for blocks a <= b:
+     *   U_aa = (I + M_aa)^-1                      (back substitution)
+     *   U_ab = -U_aa W,  W = sum_{c=a+1..b} M_ac U_cb   (by increasing b - a)
+     * so T_ba = U_ab^T = -W^T U_aa^T.  LDS (in the K / Q rows' space):
+     * MB the 10 upper blocks of M per value head, TB the 10 lower blocks of
+     * T, UD the diagonal blocks of U row-major; a block is 16 rows of BS
+     * floats (row stride 20 = 4 x odd: conflict-free 16-byte operand reads). */
+    float *MB = sbuf, *TB = sbuf + 2 * 10 * BLK, *UD = sbuf + 4 * 10 * BLK;
+
+    /* M blocks from the K K^T tiles: tile (tr >= tc) holds A[r][s] for r in
+     * block tr, s in block tc, i.e. M block (tc, tr), row s, columns r;
+     * Pm[r][s] = exp(G_r - G_s) q_r.k_s (s <= r) straight to its buffer */
 #pragma unroll
     for (int k = 0; k < 5; k++) {
         const int n = w + 4 * k, m = n % 10;
@@ -230,54 +244,91 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         const int s = 16 * tc + l16;
 #pragma unroll
         for (int v = 0; v < 2; v++) {
-            float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C;
+            float o[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = 16 * tr + 4 * lq + i;
                 const float dec = expf((float)(sG[v][r] - sG[v][s]));
-                if (n < 10)
-                    sAT[v * C * AS + s * AS + r] = s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f;
-                else
-                    Pm[r * C + s] = s <= r ? dec * res[k][i] : 0.0f;
+                o[i] = n < 10 ? (s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f)
+                              : (s <= r ? dec * res[k][i] : 0.0f);
+            }
+            if (n < 10) {
+                *reinterpret_cast<float4 *>(&MB[(v * 10 + blk_q(tc, tr)) * BLK + l16 * BS + 4 * lq]) =
+                    make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+                float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C;
+#pragma unroll
+                for (int i = 0; i < 4; i++) Pm[(16 * tr + 4 * lq + i) * C + s] = o[i];
             }
         }
     }
     q35_lds_barrier();
 
-    /* T = (I + A)^-1 by forward substitution on the identity: waves 0 and 1
-     * (value heads 0 and 1), column j on lane j.  Right-looking: once x_s
-     * is final it is applied to every later row, so each step is up to 63
-     * independent FMAs (column s of A is row s of A^T, read four entries at
-     * a time, the same address across the wave). */
-    float x[C];
-    const int j = lane;
-    if (w < 2) {
-        const float *A = sAT + w * C * AS;
+    /* diagonal blocks: wave w inverts block a = w of both value heads,
+     * column kc of U_aa on lane kc (+16 for head 1; lanes 32-63 repeat
+     * lanes 0-31 and do not write) */
+    {
+        const int a = w, v = (lane >> 4) & 1, kc = lane & 15;
+        const float *Md = MB + (v * 10 + blk_q(a, a)) * BLK;
+        float u[16];
 #pragma unroll
-        for (int r = 0; r < C; r++) x[r] = r == j ? 1.0f : 0.0f;
+        for (int s = 15; s >= 0; s--) {
+            float4 mrow[4];
 #pragma unroll
-        for (int s = 0; s < C - 1; s++) {
-            const float xs = x[s];
+            for (int q = 0; q < 4; q++) mrow[q] = *reinterpret_cast<const float4 *>(&Md[s * BS + 4 * q]);
+            float acc = s == kc ? 1.0f : 0.0f;
 #pragma unroll
-            for (int r4 = ((s + 1) >> 2) << 2; r4 < C; r4 += 4) {
-                const float4 a4 = *reinterpret_cast<const float4 *>(&A[s * AS + r4]);
+            for (int r = s + 1; r < 16; r++) acc = fmaf(-el(mrow[r >> 2], r & 3), u[r], acc);
+            u[s] = acc;
+        }
+        if (lane < 32) {
+            float *Td = TB + (v * 10 + blk_q(a, a)) * BLK + kc * BS;     /* T_aa row kc */
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (r4 + e > s) x[r4 + e] = fmaf(-el(a4, e), xs, x[r4 + e]);
-            }
+            for (int q = 0; q < 4; q++)
+                *reinterpret_cast<float4 *>(&Td[4 * q]) = make_float4(u[4 * q], u[4 * q + 1], u[4 * q + 2], u[4 * q + 3]);
+            float *Ud = UD + (v * 4 + a) * BLK;
+#pragma unroll
+            for (int s = 0; s < 16; s++) Ud[s * BS + kc] = u[s];
         }
     }
-    q35_lds_barrier();                       /* A^T no longer read */
-    if (w < 2) {
-#pragma unroll
-        for (int r = 0; r < C; r++) sbuf[w * C * AS + r * AS + j] = x[r];
-    }
     q35_lds_barrier();
-    /* T rows out: 2 heads x 64 rows x 16 float4 */
+
+    /* off-diagonal blocks by distance d = b - a: jobs (head v, block a),
+     * dealt round-robin over the waves; each is two 16x16x16 products */
+#pragma unroll
+    for (int d = 1; d < 4; d++) {
+        for (int j = w; j < 2 * (4 - d); j += 4) {
+            const int v = j / (4 - d), a = j % (4 - d), b = a + d;
+            f32x4_t wacc = {0.f, 0.f, 0.f, 0.f};
+            for (int cb = a + 1; cb <= b; cb++) {
+                /* X = M_ac row-major; Y = U_cb, read as its transpose T_bc */
+                const float4 xa = *reinterpret_cast<const float4 *>(&MB[(v * 10 + blk_q(a, cb)) * BLK + l16 * BS + 4 * lq]);
+                const float4 yb = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(cb, b)) * BLK + l16 * BS + 4 * lq]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) wacc = mfma4(el(xa, e), el(yb, e), wacc);
+            }
+            /* T_ba = (-W^T) U_aa^T: this lane's W entries W[4lq+e][l16] are
+             * X[l16][4lq+e] of -W^T as they stand; Y^T = U_aa row-major */
+            const float4 ud = *reinterpret_cast<const float4 *>(&UD[(v * 4 + a) * BLK + l16 * BS + 4 * lq]);
+            f32x4_t tb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) tb = mfma4(-wacc[e], el(ud, e), tb);
+            float *Tt = TB + (v * 10 + blk_q(a, b)) * BLK;
+#pragma unroll
+            for (int i = 0; i < 4; i++) Tt[(4 * lq + i) * BS + l16] = tb[i];
+        }
+        q35_lds_barrier();
+    }
+
+    /* T rows out: 2 heads x 64 rows x 16 float4; blocks above the diagonal
+     * are zero */
 #pragma unroll
     for (int u = 0; u < 8; u++) {
         const int idx = u * 256 + t, v = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
-        const float4 o = *reinterpret_cast<const float4 *>(&sbuf[v * C * AS + r * AS + c4]);
+        const int bb = r >> 4, ba = c4 >> 4;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (bb >= ba)
+            o = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(ba, bb)) * BLK + (r & 15) * BS + (c4 & 15)]);
         *reinterpret_cast<float4 *>(p.T + ((size_t)c * VH + 2 * kh + v) * C * C + r * C + c4) = o;
     }
 }
