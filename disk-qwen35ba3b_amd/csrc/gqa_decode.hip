@@ -34,10 +34,7 @@
 namespace {
 
 constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
-#ifndef Q35_GQA_NW
-#define Q35_GQA_NW 8        /* waves per workgroup */
-#endif
-constexpr int NW = Q35_GQA_NW, NT = 64 * NW;
+constexpr int NW = 8, NT = 64 * NW;   /* waves per workgroup, threads */
 constexpr int HPW = G / NW;           /* q heads normed per wave in the prologue */
 constexpr int MAX_CHUNKS = 256;
 constexpr int OS = 9;                 /* sO row stride (8 heads + 1): conflict-free */
