@@ -26,16 +26,18 @@
  *   chunk_kernel per (chunk, key head), all in parallel: K K^T and Q K^T
  *                on fp32 MFMA (shared by the key head's two value heads),
  *                then per value head A, Pm, the decay vectors and T by
- *                forward substitution; the last chunk's workgroups also
- *                write the last min(B, 4) raw rows into the conv ring
+ *                16x16 blocks (diagonal blocks by back substitution, the
+ *                rest on fp32 MFMA); the last chunk's workgroups also write
+ *                the last min(B, 4) raw rows into the conv ring
  *   scan_kernel  per (value head, 16-column block of vd), sequential over
  *                chunks: the state block stays in LDS; K S0, Q S0, Delta,
  *                O and S_end on fp32 MFMA (v_mfma_f32_16x16x4_f32); O
  *                unnormalised into out
  *   gnorm_kernel per (token, value head): RMSNormGated of out with z
  *                (src/attn_qwen.c:726-749)
- * All arithmetic is fp32 (MFMA fp32 products are exact, accumulation fp32),
- * the chunk-local cumulative log-decay is summed in double.
+ * All arithmetic is fp32 (MFMA fp32 products are exact, accumulation fp32)
+ * except the conv's SiLU and norm reciprocal (hardware exp / rcp, about
+ * 1 ulp); the chunk-local cumulative log-decay is summed in double.
  */
 #include "q35_device.h"
 #include "q35_launch.h"
