@@ -84,11 +84,14 @@ __global__ void synth_kv_kernel(uint16_t *kt, uint16_t *vt, int n_past, int t_ti
 /* element i of the logical [h][kd][vd] order -> value-major [h][vd][kd] */
 __global__ void synth_state_kernel(float *state, int heads, int kd, int vd, double sigma,
                                    uint64_t seed, uint64_t tid) {
+    /* thread i writes element i of the value-major state (coalesced); the
+     * value is element (h, r, c) of the row-major stream */
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)heads * kd * vd) return;
     const int h = (int)(i / ((int64_t)kd * vd)), rem = (int)(i % ((int64_t)kd * vd));
-    const int r = rem / vd, c = rem % vd;
-    state[((size_t)h * vd + c) * kd + r] = (float)(sigma * q35_normal(seed, tid, (uint64_t)i));
+    const int c = rem / kd, r = rem % kd;
+    const int64_t src = (int64_t)h * kd * vd + (int64_t)r * vd + c;
+    state[i] = sigma == 0.0 ? 0.0f : (float)(sigma * q35_normal(seed, tid, (uint64_t)src));
 }
 
 /* element i of [3][rows] (positions token-3..token-1) -> ring slot pos%4 */

@@ -84,6 +84,27 @@ def test_device_generator_matches_numpy():
     assert np.array_equal(u.cpu().numpy(), u_ref)
 
 
+def test_device_state_generator_matches_numpy():
+    """ds4f_hip_synth_lin_state writes the value-major device state of a
+    bound layer; synced back it is workloads.lin_state (row = key dim) to 1
+    ulp, and exactly zero for sigma 0."""
+    from ds4f_hip.lib import load
+    lib = load()
+    cache = KvCache(1, 64, with_kv=False)
+    ga = GpuAttention([1], 64, cache)
+    tid = S.tid(S.LIN_STATE, 0)
+    assert lib.ds4f_hip_synth_lin_state(0, 0.05, 5, tid, None) == 0
+    ga.sync(0, to_host=True)
+    ref = W.lin_state(LG, 5, 0)
+    ulp = np.abs(cache.lin[0].astype(np.float32).view(np.int32).astype(np.int64)
+                 - ref.astype(np.float32).view(np.int32).astype(np.int64))
+    _say(f"synth lin state: {int((ulp > 0).sum())} of {ulp.size} differ, max {int(ulp.max())} ulp")
+    assert ulp.max() <= 1
+    assert lib.ds4f_hip_synth_lin_state(0, 0.0, 5, tid, None) == 0
+    ga.sync(0, to_host=True)
+    assert not np.any(cache.lin[0])
+
+
 # ------------------------------------------------------------------ delta rule
 def test_lin_decode_single_step_full_shape():
     token = 3
