@@ -143,3 +143,34 @@ def ring_from_history(g: LinGeom, hist: np.ndarray, token: int) -> np.ndarray:
 def stack_kinds(n_layers: int = 40, interval: int = 4):
     """Per-layer kind: 2 = full GQA (layer % interval == interval-1), 1 = linear."""
     return [2 if (L + 1) % interval == 0 else 1 for L in range(n_layers)]
+
+
+def mlx4_pack(q: np.ndarray) -> np.ndarray:
+    """Pack 4-bit values (flattened, row-major) into U32 words of 8 nibbles,
+    low nibble first (src/kernels.c:104-113); the tail word is zero-padded."""
+    q = np.asarray(q, np.uint32).reshape(-1)
+    n = q.size
+    qq = np.zeros((n + 7) // 8 * 8, np.uint32)
+    qq[:n] = q & 0xF
+    qq = qq.reshape(-1, 8)
+    return (qq << (4 * np.arange(8, dtype=np.uint32))).sum(axis=1, dtype=np.uint64).astype(np.uint32)
+
+
+def mlx4_matrix(R: int, C: int, seed: int = 0, layer: int = 0, bias: bool = True):
+    """A synthetic MLX 4-bit affine [R x C] matrix: (vals U32, scales BF16,
+    biases BF16 or None).  q uniform in 0..15; per 64-element group a scale
+    in U(0.002, 0.02) and a bias of -scale * U(6, 9), the shape an affine
+    quantiser gives a zero-centred weight group (w = q * scale + bias)."""
+    n, ng = R * C, (R * C + 63) // 64
+    q = (S.draws(seed, S.tid(S.MLX4_Q, layer), 0, n) >> np.uint64(60)).astype(np.uint32)
+    sc = S.uniform(seed, S.tid(S.MLX4_SCALE, layer), ng, 0.002, 0.02)
+    scales = S.bf16_bits(sc)
+    biases = None
+    if bias:
+        biases = S.bf16_bits(-S.bits_to_f32(scales) * S.uniform(seed, S.tid(S.MLX4_BIAS, layer), ng, 6.0, 9.0))
+    return mlx4_pack(q), scales, biases
+
+
+def mlx4_x(C: int, seed: int = 0, layer: int = 0, step: int = 0) -> np.ndarray:
+    """An input vector N(0, 1) of the matvec (fp32)."""
+    return S.normal(seed, S.tid(S.MLX4_X, layer, step), C)

@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke() and
 by bench.py's cpu_baseline leg, always as the checker or the timed CPU
 baseline, never as a path that produces product results.  The C sources it
 binds (q35_oracle.c) restate src/attn_qwen.c gqa_body (:235-397) and
-lin_body (:434-764) with the projections removed.
+lin_body (:434-764) with the projections removed, and the MLX 4-bit matvec
+of src/kernels.c (:118-219) that the projections and the output head use.
 """
 from __future__ import annotations
 
@@ -52,6 +53,11 @@ def lib():
         L.orc_rope_table.restype = None
         L.orc_rmsnorm.argtypes = [_u16p, i, _f32p]
         L.orc_rmsnorm.restype = None
+        vp = ctypes.c_void_p
+        L.orc_mlx4_decode.argtypes = [vp, vp, vp, i, vp]
+        L.orc_mlx4_decode.restype = None
+        L.orc_mlx4_matvec.argtypes = [vp, vp, vp, i, i, vp, vp]
+        L.orc_mlx4_matvec.restype = None
         _lib = L
     return _lib
 
@@ -138,3 +144,26 @@ def rope_table(token, rd=64, theta=1e7):
     s = np.zeros(rd // 2, np.float32)
     lib().orc_rope_table(token, rd, theta, c, s)
     return c, s
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def mlx4_decode(vals, scales, biases, n):
+    """Dequantised elements 0..n-1 of an MLX 4-bit matrix (flattened)."""
+    vals, scales = _c(vals, np.uint32), _c(scales, np.uint16)
+    biases = None if biases is None else _c(biases, np.uint16)
+    out = np.empty(n, np.float32)
+    lib().orc_mlx4_decode(_ptr(vals), _ptr(scales), _ptr(biases), n, _ptr(out))
+    return out
+
+
+def mlx4_matvec(vals, scales, biases, R, C, x):
+    """y = W x for the MLX 4-bit [R x C] matrix (vals, scales, biases)."""
+    vals, scales, x = _c(vals, np.uint32), _c(scales, np.uint16), _c(x, np.float32)
+    biases = None if biases is None else _c(biases, np.uint16)
+    assert vals.size >= (R * C + 7) // 8 and scales.size >= (R * C + 63) // 64 and x.size >= C
+    y = np.empty(R, np.float32)
+    lib().orc_mlx4_matvec(_ptr(vals), _ptr(scales), _ptr(biases), R, C, _ptr(x), _ptr(y))
+    return y

@@ -276,3 +276,43 @@ int orc_lin_prefill(int k_heads, int v_heads, int kd, int vd, int t0, int B,
     }
     return 0;
 }
+
+/* ---- MLX 4-bit affine matvec (src/kernels.c:118-136, :196-219) ---- */
+
+static void mlx4_lut(const uint16_t *scales, const uint16_t *biases, long g, float lut[16]) {
+    const float sc = orc_bf16_f(scales[g]);
+    const float bi = biases ? orc_bf16_f(biases[g]) : 0.0f;
+    for (int q = 0; q < 16; q++) lut[q] = (float)q * sc + bi;
+}
+
+void orc_mlx4_decode(const uint32_t *vals, const uint16_t *scales,
+                     const uint16_t *biases, int n, float *out) {
+    float lut[16];
+    long gcur = -1;
+    for (int k = 0; k < n; k++) {
+        const long g = k / 64;
+        if (g != gcur) {
+            gcur = g;
+            mlx4_lut(scales, biases, g, lut);
+        }
+        out[k] = lut[(vals[k >> 3] >> (4 * (k & 7))) & 0xFu];
+    }
+}
+
+void orc_mlx4_matvec(const uint32_t *vals, const uint16_t *scales,
+                     const uint16_t *biases, int R, int C, const float *x, float *y) {
+    float lut[16];
+    long gcur = -1;
+    for (int r = 0; r < R; r++) {
+        float acc = 0.0f;
+        for (int c = 0; c < C; c++) {
+            const long k = (long)r * C + c, g = k / 64;
+            if (g != gcur) {
+                gcur = g;
+                mlx4_lut(scales, biases, g, lut);
+            }
+            acc += lut[(vals[k >> 3] >> (4 * (int)(k & 7))) & 0xFu] * x[c];
+        }
+        y[r] = acc;
+    }
+}

@@ -89,6 +89,20 @@ int orc_lin_prefill(int k_heads, int v_heads, int kd, int vd, int t0, int B,
                     const float *A_log, const uint16_t *dt_bias,
                     const uint16_t *norm_w, float *out);
 
+/* MLX 4-bit affine weights (src/kernels.c:104-136): U32 words of 8
+ * nibbles, low nibble first, element k = (v[k/8] >> 4(k%8)) & 15 of the
+ * row-major [R x C] matrix; BF16 scale and bias per 64 elements, group
+ * g = k / 64 over the flattened index; w = q * scale + bias (no offset).
+ * biases may be NULL (bias 0). */
+void orc_mlx4_decode(const uint32_t *vals, const uint16_t *scales,
+                     const uint16_t *biases, int n, float *out);
+
+/* y[r] = sum_c w(r, c) x[c], the scalar path of ds4f_mlx4_matvec
+ * (src/kernels.c:196-219): per-group LUT q * s + b, fp32 accumulation in
+ * ascending c. */
+void orc_mlx4_matvec(const uint32_t *vals, const uint16_t *scales,
+                     const uint16_t *biases, int R, int C, const float *x, float *y);
+
 #ifdef __cplusplus
 }
 #endif
