@@ -61,6 +61,8 @@ static void set_err(const char *fmt, ...) {
 
 const char *ds4f_gpu_last_error(void) { return P.err; }
 
+static void mlx4_free(void);
+
 #define HIPCHK(call)                                                              \
     do {                                                                          \
         hipError_t e_ = (call);                                                   \
@@ -122,6 +124,7 @@ void ds4f_gpu_free(void) {
     if (P.d_stage) hipFree(P.d_stage);
     if (P.h_stage) hipHostFree(P.h_stage);
     if (P.d_ws) hipFree(P.d_ws);
+    mlx4_free();
     hipStreamDestroy(P.stream);
     memset(&P, 0, sizeof P);
 }
@@ -679,17 +682,182 @@ int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid, v
     return 0;
 }
 
-/* ---- output-head matvecs: not part of this plugin (gpu_stub.c semantics) */
+/* ---- MLX 4-bit matvecs (include/ds4f/gpu.h:29-54) ---------------------- */
+
+/* one device copy of an MLX 4-bit weight: nibble words, scales, biases */
+typedef struct {
+    const void *key;
+    int R, C, has_b;
+    void *d;                   /* vals | scales | biases, one allocation */
+} Mlx4W;
+
+static struct {
+    Mlx4W head;                /* ds4f_gpu_mlx4_matvec's weight */
+    Mlx4W *slot;               /* ds4f_gpu_mlx4_batch's weights, by id */
+    int n_slot, cap_slot;
+    float *d_x, *d_y, *h_x, *h_y;
+    size_t x_cap, y_cap;       /* floats */
+    Q35Mlx4Job *d_jobs, *h_jobs;
+    int jobs_cap;
+} M;
+
+static size_t mlx4_vbytes(int R, int C) { return (size_t)R * C / 2; }
+static size_t mlx4_sbytes(int R, int C) { return ((size_t)R * C + 63) / 64 * 2; }
+static const uint32_t *mlx4_v(const Mlx4W *w) { return (const uint32_t *)w->d; }
+static const uint16_t *mlx4_s(const Mlx4W *w) {
+    return (const uint16_t *)((const char *)w->d + mlx4_vbytes(w->R, w->C));
+}
+static const uint16_t *mlx4_b(const Mlx4W *w) {
+    return w->has_b ? (const uint16_t *)((const char *)w->d + mlx4_vbytes(w->R, w->C) +
+                                         mlx4_sbytes(w->R, w->C))
+                    : NULL;
+}
+
+/* (re)fill a device weight from host arrays when its key or shape changed */
+static int mlx4_upload(Mlx4W *w, const void *key, const uint32_t *vals, const uint16_t *scales,
+                       const uint16_t *biases, int R, int C) {
+    const int has_b = biases != NULL;
+    if (w->d && w->key == key && w->R == R && w->C == C && w->has_b == has_b) return 0;
+    if (w->d) hipFree(w->d);
+    w->d = NULL;
+    const size_t vb = mlx4_vbytes(R, C), sb = mlx4_sbytes(R, C);
+    HIPCHK(hipMalloc(&w->d, vb + sb * (has_b ? 2 : 1)));
+    HIPCHK(hipMemcpy(w->d, vals, vb, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy((char *)w->d + vb, scales, sb, hipMemcpyHostToDevice));
+    if (has_b) HIPCHK(hipMemcpy((char *)w->d + vb + sb, biases, sb, hipMemcpyHostToDevice));
+    w->key = key;
+    w->R = R;
+    w->C = C;
+    w->has_b = has_b;
+    return 0;
+}
+
+/* pinned host and device staging for njobs x / y vectors */
+static int mlx4_stage(size_t xf, size_t yf, int njobs) {
+    if (xf > M.x_cap) {
+        if (M.d_x) hipFree(M.d_x);
+        if (M.h_x) hipHostFree(M.h_x);
+        M.d_x = M.h_x = NULL;
+        M.x_cap = 0;
+        HIPCHK(hipMalloc((void **)&M.d_x, xf * sizeof(float)));
+        HIPCHK(hipHostMalloc((void **)&M.h_x, xf * sizeof(float), hipHostMallocDefault));
+        M.x_cap = xf;
+    }
+    if (yf > M.y_cap) {
+        if (M.d_y) hipFree(M.d_y);
+        if (M.h_y) hipHostFree(M.h_y);
+        M.d_y = M.h_y = NULL;
+        M.y_cap = 0;
+        HIPCHK(hipMalloc((void **)&M.d_y, yf * sizeof(float)));
+        HIPCHK(hipHostMalloc((void **)&M.h_y, yf * sizeof(float), hipHostMallocDefault));
+        M.y_cap = yf;
+    }
+    if (njobs > M.jobs_cap) {
+        if (M.d_jobs) hipFree(M.d_jobs);
+        if (M.h_jobs) hipHostFree(M.h_jobs);
+        M.d_jobs = M.h_jobs = NULL;
+        M.jobs_cap = 0;
+        HIPCHK(hipMalloc((void **)&M.d_jobs, (size_t)njobs * sizeof(Q35Mlx4Job)));
+        HIPCHK(hipHostMalloc((void **)&M.h_jobs, (size_t)njobs * sizeof(Q35Mlx4Job),
+                             hipHostMallocDefault));
+        M.jobs_cap = njobs;
+    }
+    return 0;
+}
+
+static int mlx4_ready(int R, int C) {
+    if (!P.ok) {
+        set_err("plugin not initialised (ds4f_gpu_init)");
+        return -1;
+    }
+    if (!q35_mlx4_supported(R, C)) {
+        set_err("mlx4 matvec: unsupported shape R %d C %d (needs C %% 32 == 0, 32..8192)", R, C);
+        return -1;
+    }
+    return 0;
+}
+
+static void mlx4_free(void) {
+    if (M.head.d) hipFree(M.head.d);
+    for (int i = 0; i < M.n_slot; i++)
+        if (M.slot[i].d) hipFree(M.slot[i].d);
+    free(M.slot);
+    if (M.d_x) hipFree(M.d_x);
+    if (M.d_y) hipFree(M.d_y);
+    if (M.d_jobs) hipFree(M.d_jobs);
+    if (M.h_x) hipHostFree(M.h_x);
+    if (M.h_y) hipHostFree(M.h_y);
+    if (M.h_jobs) hipHostFree(M.h_jobs);
+    memset(&M, 0, sizeof M);
+}
+
 int ds4f_gpu_mlx4_matvec(const uint32_t *vals, const uint16_t *scales, const uint16_t *biases,
                          int R, int C, const float *x, float *y) {
-    (void)vals; (void)scales; (void)biases; (void)R; (void)C; (void)x; (void)y;
-    return -1;
+    if (mlx4_ready(R, C) != 0) return -1;
+    /* the weight stays on the device between calls (the output head); a
+     * new pointer or shape replaces it */
+    if (mlx4_upload(&M.head, vals, vals, scales, biases, R, C) != 0) return -1;
+    if (mlx4_stage((size_t)C, (size_t)R, 0) != 0) return -1;
+    memcpy(M.h_x, x, (size_t)C * sizeof(float));
+    HIPCHK(hipMemcpyAsync(M.d_x, M.h_x, (size_t)C * sizeof(float), hipMemcpyHostToDevice, P.stream));
+    Q35Mlx4 p = {mlx4_v(&M.head), mlx4_s(&M.head), mlx4_b(&M.head), M.d_x, M.d_y, NULL, R, C};
+    HIPCHK(q35_mlx4_matvec(&p, 1, P.stream));
+    HIPCHK(hipMemcpyAsync(M.h_y, M.d_y, (size_t)R * sizeof(float), hipMemcpyDeviceToHost, P.stream));
+    HIPCHK(hipStreamSynchronize(P.stream));
+    memcpy(y, M.h_y, (size_t)R * sizeof(float));
+    return 0;
 }
 
 int ds4f_gpu_mlx4_batch(const uint32_t *const *vals, const uint16_t *const *scales,
                         const uint16_t *const *biases, const float *const *xs, float *const *ys,
                         const void *const *ids, int R, int C, int njobs) {
-    (void)vals; (void)scales; (void)biases; (void)xs; (void)ys; (void)ids;
-    (void)R; (void)C; (void)njobs;
-    return -1;
+    if (njobs < 1) return 0;
+    if (mlx4_ready(R, C) != 0) return -1;
+    if (mlx4_stage((size_t)njobs * C, (size_t)njobs * R, njobs) != 0) return -1;
+    for (int j = 0; j < njobs; j++) {
+        /* weights are cached per stable id (gpu.h:36-43): the first sight
+         * uploads, later calls reuse the device copy */
+        int i = 0;
+        while (i < M.n_slot && M.slot[i].key != ids[j]) i++;
+        if (i == M.n_slot) {
+            if (M.n_slot == M.cap_slot) {
+                const int cap = M.cap_slot ? 2 * M.cap_slot : 64;
+                Mlx4W *ns = (Mlx4W *)realloc(M.slot, (size_t)cap * sizeof(Mlx4W));
+                if (!ns) {
+                    set_err("mlx4 batch: out of host memory");
+                    return -1;
+                }
+                memset(ns + M.cap_slot, 0, (size_t)(cap - M.cap_slot) * sizeof(Mlx4W));
+                M.slot = ns;
+                M.cap_slot = cap;
+            }
+            M.n_slot++;
+        }
+        if (mlx4_upload(&M.slot[i], ids[j], vals[j], scales[j], biases ? biases[j] : NULL, R, C) != 0)
+            return -1;
+        memcpy(M.h_x + (size_t)j * C, xs[j], (size_t)C * sizeof(float));
+        const Q35Mlx4Job jb = {mlx4_v(&M.slot[i]), mlx4_s(&M.slot[i]), mlx4_b(&M.slot[i]),
+                               M.d_x + (size_t)j * C, M.d_y + (size_t)j * R};
+        M.h_jobs[j] = jb;
+    }
+    HIPCHK(hipMemcpyAsync(M.d_x, M.h_x, (size_t)njobs * C * sizeof(float), hipMemcpyHostToDevice,
+                          P.stream));
+    HIPCHK(hipMemcpyAsync(M.d_jobs, M.h_jobs, (size_t)njobs * sizeof(Q35Mlx4Job),
+                          hipMemcpyHostToDevice, P.stream));
+    Q35Mlx4 p = {NULL, NULL, NULL, NULL, NULL, M.d_jobs, R, C};
+    HIPCHK(q35_mlx4_matvec(&p, njobs, P.stream));
+    HIPCHK(hipMemcpyAsync(M.h_y, M.d_y, (size_t)njobs * R * sizeof(float), hipMemcpyDeviceToHost,
+                          P.stream));
+    HIPCHK(hipStreamSynchronize(P.stream));
+    for (int j = 0; j < njobs; j++) memcpy(ys[j], M.h_y + (size_t)j * R, (size_t)R * sizeof(float));
+    return 0;
+}
+
+int ds4f_hip_mlx4_matvec_async(const uint32_t *vals, const uint16_t *scales,
+                               const uint16_t *biases, int R, int C, const float *x, float *y,
+                               void *stream) {
+    if (mlx4_ready(R, C) != 0) return -1;
+    Q35Mlx4 p = {vals, scales, biases, x, y, NULL, R, C};
+    HIPCHK(q35_mlx4_matvec(&p, 1, pick(stream)));
+    return 0;
 }

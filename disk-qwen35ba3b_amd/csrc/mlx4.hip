@@ -1,0 +1,149 @@
+/*
+ * mlx4.hip -- MLX 4-bit affine matvec on gfx950: y = W x for the
+ * [R x C] weight of src/kernels.c:104-219 (ds4f_mlx4_matvec) and its
+ * batched form (the routed-expert jobs of ds4f_gpu_mlx4_batch,
+ * include/ds4f/gpu.h:29-54).
+ *
+ * Format: U32 words of 8 nibbles, low nibble first; element k = r*C + c
+ * of the flattened matrix is nibble k%8 of word k/8; a BF16 scale and bias
+ * per 64 elements (group k/64, which may straddle rows); w = q*scale+bias.
+ *
+ * One wave per row, two rows in flight per iteration; lane l takes 32
+ * consecutive elements (one 16-byte word load) of each 2048-column chunk.
+ * With C % 32 == 0 those 32 elements start 32-aligned in the flattened
+ * index, so they lie in one group: the lane computes
+ *     scale * sum_e q_e x_e + bias * sum_e x_e
+ * with x and its per-lane sums held in registers for every row the wave
+ * visits.  The products are fp32 FMAs on the integer nibbles (exact), the
+ * sums fp32; the summation order differs from the reference's per-element
+ * q*s+b accumulation, a float32 rounding difference (gpu.h:13-18).
+ * The row's partial sums meet in a DPP wave reduction.  HBM-bound: R*C/2
+ * bytes of nibbles plus R*C/16 bytes of scales and biases per matvec.
+ */
+#include "q35_device.h"
+#include "q35_launch.h"
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int CHUNK = 2048;            /* columns per 64 lanes x 32 */
+constexpr int MAXCH = 4;               /* C <= 8192 */
+
+struct Mlx4Job {
+    const uint32_t *vals;
+    const uint16_t *scales, *biases;
+    const float *x;
+    float *y;
+};
+
+/* 32 nibble products of one lane: 4 words, 8 nibbles each, against x[32] */
+__device__ __forceinline__ float nib_dot(u32x4_t w, const float (&x)[32]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            acc = fmaf((float)((lo >> (8 * b)) & 0xFFu), x[8 * i + 2 * b], acc);
+            acc = fmaf((float)((hi >> (8 * b)) & 0xFFu), x[8 * i + 2 * b + 1], acc);
+        }
+    }
+    return acc;
+}
+
+template <int NCH>
+__global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
+    Mlx4Job j;
+    if (p.jobs) {
+        const Q35Mlx4Job &d = p.jobs[blockIdx.y];
+        j = {d.vals, d.scales, d.biases, d.x, d.y};
+    } else {
+        j = {p.vals, p.scales, p.biases, p.x, p.y};
+    }
+    const int R = p.R, C = p.C, lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * (NT / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (NT / 64);
+
+    /* x of this lane's columns and their sums, per chunk */
+    float xr[NCH][32], xs[NCH];
+    bool live[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ch++) {
+        const int c0 = ch * CHUNK + 32 * lane;
+        live[ch] = c0 < C;
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const float4 v = live[ch] ? *reinterpret_cast<const float4 *>(j.x + c0 + 4 * q)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            xr[ch][4 * q] = v.x;
+            xr[ch][4 * q + 1] = v.y;
+            xr[ch][4 * q + 2] = v.z;
+            xr[ch][4 * q + 3] = v.w;
+            s += (v.x + v.y) + (v.z + v.w);
+        }
+        xs[ch] = s;
+    }
+
+    /* range-checked views: rows at and past R read zero */
+    const size_t nel = (size_t)R * C;
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint32_t *>(j.vals)), 0, (int)(nel / 2), Q35_BUF_DW3);
+    const int ng = (int)((nel + 63) / 64);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(j.scales)), 0, 2 * ng, Q35_BUF_DW3);
+    const bool has_b = j.biases != nullptr;
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(has_b ? j.biases : j.scales)), 0, has_b ? 2 * ng : 0, Q35_BUF_DW3);
+
+    for (int r0 = 2 * wave; r0 < R; r0 += 2 * nwaves) {
+        float part[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int r = r0 + u;                      /* may be R: reads zero */
+            float acc = 0.0f;
+#pragma unroll
+            for (int ch = 0; ch < NCH; ch++) {
+                /* element index of this lane's first column; a dead lane
+                 * (column >= C) points past the buffer and reads zero */
+                const int64_t k0 = (int64_t)r * C + ch * CHUNK + 32 * lane;
+                const int kk = live[ch] ? (int)(k0 >> 3) : (int)(nel / 8);
+                const int gg = live[ch] ? (int)(k0 >> 6) : ng;
+                const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(vr, 4 * kk, 0, 0);
+                const float sc = q35_bf2f((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(sr, 2 * gg, 0, 0));
+                const float bi = q35_bf2f((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(br, 2 * gg, 0, 0));
+                acc = fmaf(sc, nib_dot(w, xr[ch]), fmaf(bi, xs[ch], acc));
+            }
+            part[u] = acc;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float t = q35_wave_sum(part[u]);
+            if (lane == 0 && r0 + u < R) j.y[r0 + u] = t;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int q35_mlx4_supported(int R, int C) {
+    return R >= 1 && C >= 32 && C % 32 == 0 && C <= MAXCH * CHUNK &&
+           (int64_t)R * C / 2 < ((int64_t)1 << 31);
+}
+
+extern "C" hipError_t q35_mlx4_matvec(const Q35Mlx4 *p, int njobs, hipStream_t stream) {
+    if (!q35_mlx4_supported(p->R, p->C) || njobs < 1 || (njobs > 1 && !p->jobs))
+        return hipErrorInvalidValue;
+    /* enough waves to keep the HBM pipes full, at least one row pair each */
+    int64_t pairs = ((int64_t)p->R + 1) / 2;
+    int64_t blocks = (pairs + NT / 64 - 1) / (NT / 64);
+    if (blocks > 2048) blocks = 2048;
+    const dim3 grid((unsigned)blocks, (unsigned)njobs);
+    const int nch = (p->C + CHUNK - 1) / CHUNK;
+    if (nch == 1)
+        hipLaunchKernelGGL(mlx4_kernel<1>, grid, dim3(NT), 0, stream, *p);
+    else if (nch == 2)
+        hipLaunchKernelGGL(mlx4_kernel<2>, grid, dim3(NT), 0, stream, *p);
+    else
+        hipLaunchKernelGGL(mlx4_kernel<4>, grid, dim3(NT), 0, stream, *p);
+    return hipGetLastError();
+}

@@ -122,8 +122,31 @@ hipError_t q35_synth_state(float *state, int heads, int kd, int vd, double sigma
 hipError_t q35_synth_conv(float *ring, int rows, int token, uint64_t seed, uint64_t tid,
                           hipStream_t stream);
 
+/* ---- MLX 4-bit affine matvec (src/kernels.c:104-219) ---- *
+ * y[R] = W[R x C] x, W as U32 nibble words + BF16 scale / bias per 64
+ * elements (biases may be NULL).  One job: the inline pointers, jobs NULL.
+ * Batched: jobs points to njobs device descriptors sharing R and C. */
+typedef struct Q35Mlx4Job {
+    const uint32_t *vals;
+    const uint16_t *scales, *biases;
+    const float *x;
+    float *y;
+} Q35Mlx4Job;
+typedef struct Q35Mlx4 {
+    const uint32_t *vals;
+    const uint16_t *scales, *biases;
+    const float *x;
+    float *y;
+    const Q35Mlx4Job *jobs;        /* device array, or NULL for the inline job */
+    int R, C;
+} Q35Mlx4;
+/* 1 if the kernel takes this shape: C % 32 == 0, 32 <= C <= 8192 */
+int q35_mlx4_supported(int R, int C);
+hipError_t q35_mlx4_matvec(const Q35Mlx4 *p, int njobs, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
+
 
 #endif /* Q35_LAUNCH_H */

@@ -175,19 +175,39 @@ int ds4f_hip_synth_lin_state(int L, double sigma, uint64_t seed, uint64_t tid,
 int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid,
                                 void *stream);
 
-/* ---- the rest of include/ds4f/gpu.h (:29-54) -------------------------- *
- * The output-head MLX-4bit matvecs are outside this plugin: they return -1
- * (unavailable), exactly as src/gpu_stub.c does, so the engine keeps its
- * CPU matvec.  They are exported so this library can stand in for
- * gpu_stub.c in the engine's GPU_SRC slot. */
+/* ---- the MLX-4bit matvecs of include/ds4f/gpu.h (:29-54) --------------- *
+ * y = W x for an MLX 4-bit affine [R x C] weight in the layout of
+ * ds4f_mlx4_matvec (src/kernels.c:104-219): U32 words of 8 nibbles, low
+ * nibble first, BF16 scale and optional BF16 bias per 64 elements of the
+ * flattened matrix, w = q * scale + bias.  Host pointers; the result is in
+ * y on return.  Shapes with C % 32 == 0 and 32 <= C <= 8192 run on the
+ * GPU; any other shape, or an uninitialised plugin, returns -1 (the
+ * caller runs its CPU matvec), as gpu.h specifies.  Results differ from
+ * the CPU path by float32 summation order only (gpu.h:13-18).
+ *
+ * ds4f_gpu_mlx4_matvec replaces the Metal/stub function of the same name
+ * (src/gpu_metal.mm:83-128, src/gpu_stub.c); the weight is uploaded once
+ * and kept on the device while the vals pointer and shape stay the same
+ * (the output head). */
 int ds4f_gpu_mlx4_matvec(const uint32_t *vals, const uint16_t *scales,
                          const uint16_t *biases, int R, int C,
                          const float *x, float *y);
+/* Batched expert matvec (gpu.h:31-54): y[j] = W_j x_j, every job sharing
+ * R and C; weights are cached per stable id ids[j] (first sight uploads);
+ * one dispatch for the batch.  biases may be NULL (no biases) or hold NULL
+ * entries. */
 int ds4f_gpu_mlx4_batch(const uint32_t *const *vals,
                         const uint16_t *const *scales,
                         const uint16_t *const *biases,
                         const float *const *xs, float *const *ys,
                         const void *const *ids, int R, int C, int njobs);
+/* Device-resident form of ds4f_mlx4_matvec (src/kernels.c:158-219): all
+ * pointers are device memory, the call only enqueues on `stream` (NULL:
+ * the plugin's stream).  For callers that keep activations in HBM (the
+ * attention projections of src/attn_qwen.c:160-165, :932-948). */
+int ds4f_hip_mlx4_matvec_async(const uint32_t *vals, const uint16_t *scales,
+                               const uint16_t *biases, int R, int C,
+                               const float *x, float *y, void *stream);
 
 /* Last error text of the plugin (static storage). */
 const char *ds4f_gpu_last_error(void);
