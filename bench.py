@@ -33,6 +33,10 @@ Other workloads (one JSON line each, same fields):
                 layer, zero state and conv ring, fp32 qkv/z/a/b N(0,1);
                 chunked form on fp32 MFMA, roofline against the fp32 MFMA
                 peak.
+  mlx4_head     the MLX 4-bit affine matvec of the output head (248320 x
+                2048, 287 MB of nibbles, scales and biases: more than the
+                256 MB MALL, so the weight streams from HBM every call),
+                device-resident; HBM roofline.
 """
 from __future__ import annotations
 
@@ -80,7 +84,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill",
                                                                     "lin_prefill", "hbm_copy",
-                                                                    "gqa_decode", "lin_decode"])
+                                                                    "gqa_decode", "lin_decode",
+                                                                    "mlx4_head"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     ap.add_argument("--npast", type=int, default=4096, help="cached positions (gqa_decode)")
     ap.add_argument("--rotate", type=int, default=0,
@@ -99,6 +104,8 @@ def main() -> int:
         return run_hbm_copy(args)
     if args.workload in ("gqa_decode", "lin_decode"):
         return run_layer_decode(args)
+    if args.workload == "mlx4_head":
+        return run_mlx4_head(args)
     return run_stack_decode(args)
 
 
@@ -708,5 +715,87 @@ def run_lin_prefill(args) -> int:
     return 0
 
 
+
+def run_mlx4_head(args) -> int:
+    """y = W x for the MLX 4-bit output head (R = 248320 vocabulary rows,
+    C = 2048) through the device-resident entry; one launch per step."""
+    import numpy as np
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip.attn import dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    L.check(lib.ds4f_gpu_init(), "init")
+    R, C, seed = 248320, 2048, args.seed
+    rng = np.random.default_rng(seed)
+    ng = R * C // 64
+    vals = rng.integers(0, 1 << 32, R * C // 8, dtype=np.uint64).astype(np.uint32)
+    sc = rng.uniform(0.002, 0.02, ng).astype(np.float32)
+    scales = (sc.view(np.uint32) >> 16).astype(np.uint16)
+    biases = ((-sc * rng.uniform(6, 9, ng).astype(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+    x = rng.standard_normal(C).astype(np.float32)
+    dev = torch.device("cuda:0")
+    dv = torch.from_numpy(vals.view(np.int32)).to(dev)
+    ds = torch.from_numpy(scales.view(np.int16)).to(dev)
+    db = torch.from_numpy(biases.view(np.int16)).to(dev)
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.empty(R, dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    torch.cuda.set_stream(stream)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    K, WU = max(1, min(args.steps, 200)), max(1, min(args.warmup, 20))
+
+    def step():
+        L.check(lib.ds4f_hip_mlx4_matvec_async(dptr(dv), dptr(ds), dptr(db), R, C, dptr(dx),
+                                               dptr(dy), st), "mlx4")
+
+    for _ in range(WU):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(K):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / K
+    nbytes = R * C // 2 + 2 * ng * 2 + C * 4 + R * 4
+    gbps = nbytes / (us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": load_traffic("mlx4_head"),
+                "kernel": "mlx4_kernel (MLX 4-bit affine matvec)", "launches": K,
+                "us_per_launch": round(us, 2), "bytes_per_launch": nbytes}
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        rows = 8192          # a row sample of the same weight; the cost is linear in rows
+        reps, secs = 0, 0.0
+        while reps == 0 or secs < min(args.cpu_seconds, 5.0):
+            c0 = time.perf_counter()
+            O.mlx4_matvec(vals[:rows * C // 8], scales[:rows * C // 64], biases[:rows * C // 64],
+                          rows, C, x)
+            secs += time.perf_counter() - c0
+            reps += 1
+        cpu = {"value": round(reps * rows / R / secs, 3), "unit": "matvecs/s", "cores": 1,
+               "kind": "port",
+               "sample": f"{reps} oracle matvecs of the first {rows} rows of the same weight "
+                         f"({secs:.1f} s), scaled to {R} rows"}
+    line = {"metric": "MLX 4-bit output-head matvec (248320 x 2048) matvecs/s", "value": round(1e6 / us, 1),
+            "unit": "matvecs/s", "n_gpus": 1, "steps": K, "warmup": WU,
+            "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u4/bf16 weights, f32 x and accumulation",
+            "data": f"synthetic (numpy default_rng({seed}): random nibble words, scales "
+                    "U(0.002, 0.02), biases -scale * U(6, 9), x N(0, 1))",
+            "config": {"workload": "mlx4_head", "rows": R, "cols": C, "weight_bytes": nbytes - C * 4 - R * 4},
+            "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 if __name__ == "__main__":
     sys.exit(main())
+

@@ -14,7 +14,7 @@
  * index, so they lie in one group: the lane computes
  *     scale * sum_e q_e x_e + bias * sum_e x_e
  * with x and its per-lane sums held in registers for every row the wave
- * visits.  The products are fp32 FMAs on the integer nibbles (exact), the
+ * visits.  The products are fp32 FMAs on the exact nibble values, the
  * sums fp32; the summation order differs from the reference's per-element
  * q*s+b accumulation, a float32 rounding difference (gpu.h:13-18).
  * The row's partial sums meet in a DPP wave reduction.  HBM-bound: R*C/2
@@ -36,19 +36,33 @@ struct Mlx4Job {
     float *y;
 };
 
-/* 32 nibble products of one lane: 4 words, 8 nibbles each, against x[32] */
+/* 32 nibble products of one lane: 4 words, 8 nibbles each, against x[32].
+ * Masking a word with 0x0F0F0F0F leaves one nibble per byte; a byte q < 16
+ * read as an fp8 e4m3 number is q * 2^-9 exactly (exponent field 0 or 1,
+ * where e4m3 is linear), so v_cvt_pk_f32_fp8 turns two nibbles into two
+ * exact floats in one instruction.  x is held pre-multiplied by the
+ * inverse of that unit, a power of two, so each product is q * x exactly
+ * as with an integer conversion.  Byte b of the low mask is nibble 2b,
+ * of the high mask nibble 2b+1. */
 __device__ __forceinline__ float nib_dot(u32x4_t w, const float (&x)[32]) {
-    float acc = 0.0f;
+    float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            acc = fmaf((float)((lo >> (8 * b)) & 0xFFu), x[8 * i + 2 * b], acc);
-            acc = fmaf((float)((hi >> (8 * b)) & 0xFFu), x[8 * i + 2 * b + 1], acc);
-        }
+        const int lo = (int)(w[i] & 0x0F0F0F0Fu), hi = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
+        const auto l0 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);   /* nibbles 0, 2 */
+        const auto l1 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);    /* nibbles 4, 6 */
+        const auto h0 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);   /* nibbles 1, 3 */
+        const auto h1 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);    /* nibbles 5, 7 */
+        a0 = fmaf(l0[0], x[8 * i + 0], a0);
+        a1 = fmaf(h0[0], x[8 * i + 1], a1);
+        a0 = fmaf(l0[1], x[8 * i + 2], a0);
+        a1 = fmaf(h0[1], x[8 * i + 3], a1);
+        a0 = fmaf(l1[0], x[8 * i + 4], a0);
+        a1 = fmaf(h1[0], x[8 * i + 5], a1);
+        a0 = fmaf(l1[1], x[8 * i + 6], a0);
+        a1 = fmaf(h1[1], x[8 * i + 7], a1);
     }
-    return acc;
+    return a0 + a1;
 }
 
 template <int NCH>
@@ -63,7 +77,9 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
     const int R = p.R, C = p.C, lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (NT / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (NT / 64);
 
-    /* x of this lane's columns and their sums, per chunk */
+    /* x of this lane's columns (scaled by the inverse fp8 nibble unit)
+     * and their plain sums, per chunk */
+    const float xsc = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
     float xr[NCH][32], xs[NCH];
     bool live[NCH];
 #pragma unroll
@@ -75,10 +91,10 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
         for (int q = 0; q < 8; q++) {
             const float4 v = live[ch] ? *reinterpret_cast<const float4 *>(j.x + c0 + 4 * q)
                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-            xr[ch][4 * q] = v.x;
-            xr[ch][4 * q + 1] = v.y;
-            xr[ch][4 * q + 2] = v.z;
-            xr[ch][4 * q + 3] = v.w;
+            xr[ch][4 * q] = v.x * xsc;
+            xr[ch][4 * q + 1] = v.y * xsc;
+            xr[ch][4 * q + 2] = v.z * xsc;
+            xr[ch][4 * q + 3] = v.w * xsc;
             s += (v.x + v.y) + (v.z + v.w);
         }
         xs[ch] = s;
