@@ -6,13 +6,21 @@
  * decay / beta gates, the gated delta rule on the 128x128 fp32 state of
  * every value head, and the RMSNormGated epilogue.
  *
- * One workgroup owns one value head: 1024 threads, thread t holds column
- * j = t/8 of the value-major state and 16 consecutive key rows of it
- * (64 contiguous bytes).  The state is the dominant traffic (64 KiB read and
- * 64 KiB written per head); its loads are issued before the prologue so the
- * HBM latency overlaps the conv / norm work.  Owning a whole head keeps the
- * RMSNormGated reduction (over all 128 value columns) inside the workgroup,
- * so the layer is one launch with no cross-workgroup handshake.
+ * One workgroup owns one value head: 1024 threads, 16 waves; wave w holds
+ * value columns 8w..8w+7 of the value-major state (4 KiB, contiguous).  Its
+ * u-th 16-byte load and store cover kilobyte u of that range: lane l holds
+ * column 8w + 2u + (l >> 5), key rows 4(l & 31)..+3, so each instruction
+ * moves 1 KiB of whole cache lines (a column-per-8-lanes layout would have
+ * each instruction touch 32 lines partially, four times the requests).  The
+ * state is the dominant traffic (64 KiB read and 64 KiB written per head);
+ * the per-column sums over key rows are 32-lane reductions.  The state loads
+ * are issued after the prologue's few loads (returns are counted in order,
+ * so the conv does not wait for the state) and before its arithmetic.
+ * Owning a whole head keeps the RMSNormGated reduction (over all 128 value
+ * columns) inside the workgroup, so the layer is one launch with no
+ * cross-workgroup handshake: splitting a head over workgroups would need an
+ * agent-scope release / acquire per head, which costs more on this GPU than
+ * the per-CU state traffic it spreads.
  *
  * Arithmetic: fp32 with FMA in the state update (the reference sums i in
  * ascending order without FMA; the difference is fp32 rounding).  The
@@ -33,12 +41,10 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     const int tok = p.token;
 
     /* ---- every global input in flight at once ---- */
-    /* state slice: column j, key rows il*16 .. il*16+15 */
-    const int j = t >> 3, il = t & 7;
-    float4 *sp = reinterpret_cast<float4 *>(p.state + ((size_t)h * VD + j) * KD + il * 16);
+    /* state: wave w's columns 8w..8w+7; load u is kilobyte u of them */
+    const int w = t >> 6, l = t & 63, half = l >> 5, r0 = 4 * (l & 31);
+    float4 *sp = reinterpret_cast<float4 *>(p.state + ((size_t)h * VD + 8 * w) * KD) + l;
     float4 s[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) s[u] = sp[u];
     /* conv inputs of this head's q (t<128), k (t<256), v (t<384) channels */
     int ch = -1, kind = -1;
     if (t < KD) {
@@ -75,6 +81,8 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         gdt = p.dt_bias[h];
     }
 
+#pragma unroll
+    for (int u = 0; u < 4; u++) s[u] = sp[64 * u];
     __shared__ float sq[KD], sk[KD], sv[VD], so[VD];
     __shared__ double sred[4];
     __shared__ float sgate[2];
@@ -116,39 +124,44 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     }
     q35_lds_barrier();
 
-    /* ---- gated delta rule on column j (src/attn_qwen.c:666-690) ---- */
+    /* ---- gated delta rule (src/attn_qwen.c:666-690), four columns per lane ---- */
     const float dec = sgate[0], beta = sgate[1];
-    const float4 *k4 = reinterpret_cast<const float4 *>(sk + il * 16);
-    const float4 *q4 = reinterpret_cast<const float4 *>(sq + il * 16);
-    float mem = 0.0f;
+    const float4 kk = *reinterpret_cast<const float4 *>(sk + r0);
+    const float4 qq = *reinterpret_cast<const float4 *>(sq + r0);
+    float mem[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        float4 kk = k4[u];
         s[u].x *= dec; s[u].y *= dec; s[u].z *= dec; s[u].w *= dec;
-        mem = fmaf(s[u].x, kk.x, mem);
-        mem = fmaf(s[u].y, kk.y, mem);
-        mem = fmaf(s[u].z, kk.z, mem);
-        mem = fmaf(s[u].w, kk.w, mem);
+        float m = s[u].x * kk.x;
+        m = fmaf(s[u].y, kk.y, m);
+        m = fmaf(s[u].z, kk.z, m);
+        m = fmaf(s[u].w, kk.w, m);
+        mem[u] = m;
     }
-    mem = q35_sum8(mem);      /* the 8 lanes of column j */
-    const float delta = (sv[j] - mem) * beta;
-    float o = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) mem[u] = q35_half_sum(mem[u]);   /* the column's 32 lanes */
+    float o[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        float4 kk = k4[u], qq = q4[u];
+        const float delta = (sv[8 * w + 2 * u + half] - mem[u]) * beta;
         s[u].x = fmaf(kk.x, delta, s[u].x);
         s[u].y = fmaf(kk.y, delta, s[u].y);
         s[u].z = fmaf(kk.z, delta, s[u].z);
         s[u].w = fmaf(kk.w, delta, s[u].w);
-        o = fmaf(s[u].x, qq.x, o);
-        o = fmaf(s[u].y, qq.y, o);
-        o = fmaf(s[u].z, qq.z, o);
-        o = fmaf(s[u].w, qq.w, o);
+        float a = s[u].x * qq.x;
+        a = fmaf(s[u].y, qq.y, a);
+        a = fmaf(s[u].z, qq.z, a);
+        a = fmaf(s[u].w, qq.w, a);
+        o[u] = a;
     }
-    o = q35_sum8(o);
 #pragma unroll
-    for (int u = 0; u < 4; u++) sp[u] = s[u];
-    if (il == 0) so[j] = o;
+    for (int u = 0; u < 4; u++) sp[64 * u] = s[u];
+#pragma unroll
+    for (int u = 0; u < 4; u++) o[u] = q35_half_sum(o[u]);
+    if ((l & 31) == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) so[8 * w + 2 * u + half] = o[u];
+    }
     q35_lds_barrier();
 
     /* ---- RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749) ---- */
