@@ -37,7 +37,8 @@ constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
 constexpr int NW = 8, NT = 64 * NW;   /* waves per workgroup, threads */
 constexpr int HPW = G / NW;           /* q heads normed per wave in the prologue */
 constexpr int MAX_CHUNKS = 256;
-constexpr int OS = 9;                 /* sO row stride (8 heads + 1): conflict-free */
+constexpr int OS = D + 16;            /* sO head stride: head hq starts 16 hq banks on */
+static_assert(NW == 8 && G == 8, "the wave merge maps lane = 8 * head + wave");
 constexpr float SCALE = 0.0625f;      /* 1/sqrtf(256), src/attn_qwen.c:334 */
 struct KTile { bf16x8_t k[8]; };
 struct VTile { s16x4_t v[16]; };
@@ -139,11 +140,11 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     const int wv = __builtin_amdgcn_readfirstlane(w);
     const int koff = (lane & 15) * 64 + (lane >> 4) * 16, voff = (lane & 15) * 32 + (lane >> 4) * 8;
 
-    __shared__ float sQ[G][D];
+    __shared__ __align__(16) float sQ[G][D];
     __shared__ bf16x8_t sQb[8 * 64];
-    __shared__ float sO[NW][D * OS];
+    __shared__ __align__(16) float sO[NW][G * OS];
     __shared__ float sM[NW + 1][G], sL[NW + 1][G], sF[NW + 1][G];
-    __shared__ float sKn[D], sVn[D];
+    __shared__ __align__(16) float sKn[D], sVn[D];
 
     /* ---- prologue: every input in flight at once ---- */
     float4 xq[HPW];
@@ -231,13 +232,16 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     /* ---- per-wave partial: l over the 4 lane groups; O hi + lo columns ---- */
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
+    /* lane (n < 8, grp) holds dims 16dt + 4grp .. +3 of head n: one 16-byte
+     * LDS store per dim block */
 #pragma unroll
     for (int dt = 0; dt < 16; dt++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float o = acc[dt][i] + q35_xor8(acc[dt][i]);
-            if (!is_lo) sO[w][(16 * dt + 4 * grp + i) * OS + hq] = o;
-        }
+        float4 o4;
+        o4.x = acc[dt][0] + q35_xor8(acc[dt][0]);
+        o4.y = acc[dt][1] + q35_xor8(acc[dt][1]);
+        o4.z = acc[dt][2] + q35_xor8(acc[dt][2]);
+        o4.w = acc[dt][3] + q35_xor8(acc[dt][3]);
+        if (!is_lo) *reinterpret_cast<float4 *>(&sO[w][hq * OS + 16 * dt + 4 * grp]) = o4;
     }
     if (lane < G) {
         sM[w][lane] = m_run;
@@ -259,31 +263,53 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     }
     q35_lds_barrier();
 
-    /* ---- merge the waves (and the new token): 8 x 5 factors once ---- */
-    const int nsrc = last ? NW + 1 : NW;
+    /* ---- merge the waves (and the new token) ---- *
+     * wave 0, lane = 8 * head + source wave: the max and the weighted sum over
+     * the 8 lanes of a head on DPP, the new token folded in after. */
     float *po = p.part_o + ((size_t)(g * p.n_chunks + c) * G) * D;
     float *pml = p.part_ml + ((size_t)(g * p.n_chunks + c) * G) * 2;
-    if (t < G) {
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < nsrc; s2++) M = fmaxf(M, sM[s2][t]);
-        float L = 0.0f;
-        for (int s2 = 0; s2 < NW + 1; s2++) {
-            const float f =
-                (s2 >= nsrc || sM[s2][t] == -INFINITY) ? 0.0f : q35_exp(sM[s2][t] - M);
-            sF[s2][t] = f;
-            L += sL[s2][t] * f;
+    if (w == 0) {
+        const int hh = lane >> 3, s2 = lane & 7;
+        const float ms = sM[s2][hh], ls = sL[s2][hh];
+        float M = ms;
+        M = fmaxf(M, q35_dpp<0xB1>(M));
+        M = fmaxf(M, q35_dpp<0x4E>(M));
+        M = fmaxf(M, q35_dpp<0x141>(M));
+        const float mnew = last ? sM[NW][hh] : -INFINITY;
+        M = fmaxf(M, mnew);
+        const float f = (ms == -INFINITY) ? 0.0f : q35_exp(ms - M);
+        const float L = q35_sum8(ls * f);
+        sF[s2][hh] = f;
+        if (s2 == 0) {
+            const float fn = last ? q35_exp(mnew - M) : 0.0f;
+            sF[NW][hh] = fn;
+            pml[hh * 2] = M;
+            pml[hh * 2 + 1] = L + (last ? sL[NW][hh] * fn : 0.0f);
         }
-        pml[t * 2] = M;
-        pml[t * 2 + 1] = L;
     }
     q35_lds_barrier();
-    for (int e = t; e < G * D; e += NT) {
-        const int hh = e / D, d = e % D;
-        float o = sO[0][d * OS + hh] * sF[0][hh];
+    {
+        /* thread t: head t / 64, dims 4 (t % 64) .. +3 */
+        const int hh = t >> 6, d4 = 4 * lane;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int s2 = 1; s2 < NW; s2++) o += sO[s2][d * OS + hh] * sF[s2][hh];
-        if (last) o += sVn[d] * sF[NW][hh];
-        po[e] = o;
+        for (int s2 = 0; s2 < NW; s2++) {
+            const float4 v = *reinterpret_cast<const float4 *>(&sO[s2][hh * OS + d4]);
+            const float f = sF[s2][hh];
+            o.x = fmaf(v.x, f, o.x);
+            o.y = fmaf(v.y, f, o.y);
+            o.z = fmaf(v.z, f, o.z);
+            o.w = fmaf(v.w, f, o.w);
+        }
+        if (last) {
+            const float4 v = *reinterpret_cast<const float4 *>(&sVn[d4]);
+            const float f = sF[NW][hh];
+            o.x = fmaf(v.x, f, o.x);
+            o.y = fmaf(v.y, f, o.y);
+            o.z = fmaf(v.z, f, o.z);
+            o.w = fmaf(v.w, f, o.w);
+        }
+        *reinterpret_cast<float4 *>(po + hh * D + d4) = o;
     }
 }
 
