@@ -37,6 +37,7 @@
 
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 
 namespace {
 
@@ -65,6 +66,21 @@ __device__ __forceinline__ int v_key(int s) {
     const int ks = s >> 4, s16 = s & 15;
     const int r16 = ((s16 >> 3) << 2) + (s16 & 3) + ((s16 & 4) ? 8 : 0);
     return ks * 16 + r16;
+}
+
+/* fp16 key workspace: one 16 KB tile per 32 keys, granule-major (the
+ * dims 8c..8c+7 of key r at granule 32c + r).  A tile goes to LDS as it
+ * lies, and an MFMA operand read (32 keys x one granule) is 512
+ * consecutive bytes. */
+__device__ __forceinline__ size_t kw_index(int g, int kbt, int pos, int d) {
+    return ((((size_t)g * kbt + (pos >> 5)) * 32 + (d >> 3)) * 32 + (pos & 31)) * 8 + (d & 7);
+}
+
+/* fp16 value workspace: one 16 KB tile per 32 keys, dim rows of 32 key
+ * slots (4 granules); granule gr of row d is stored at gr ^ ((d >> 2) & 3),
+ * so the operand reads of 16 consecutive rows hit 16 distinct bank groups. */
+__device__ __forceinline__ size_t vw_index(int g, int kbt, int kb, int d, int slot) {
+    return (((size_t)g * kbt + kb) * D + d) * 32 + (((slot >> 3) ^ ((d >> 2) & 3)) << 3) + (slot & 7);
 }
 
 __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
@@ -101,14 +117,13 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
                                     (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
         *reinterpret_cast<uint2 *>(dst) = pk;
     }
-    const int kb = pos >> 5, kr = pos & 31;
     if (w == 0) {
 #pragma unroll
         for (int g = 0; g < 2; g++) {
             const float4 y = q35_norm_rope_head(xk[g], wk, rc, rs, lane);
             if (p.k_post)
                 *reinterpret_cast<float4 *>(p.k_post + ((size_t)b * p.kv_heads + g) * D + d0) = y;
-            uint16_t *dst = p.kw + (((size_t)g * p.kbt + kb) * 32 + kr) * D + d0;
+            uint16_t *dst = p.kw + kw_index(g, p.kbt, pos, d0);
             *reinterpret_cast<uint2 *>(dst) =
                 make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
                            (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
@@ -149,7 +164,7 @@ __global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
         const int idx = u * 256 + t, d = idx >> 5, slot = idx & 31;
         const int r = v_key(slot), pos = 32 * kb + r;
         if (pos >= p.t0 && pos < p.t0 + p.B)
-            p.vw[(((size_t)g * p.kbt + kb) * D + d) * 32 + slot] = f16_bits(sv[r][d]);
+            p.vw[vw_index(g, p.kbt, kb, d, slot)] = f16_bits(sv[r][d]);
     }
     /* cache: two 16-token tiles, lane (tile, d, token) */
 #pragma unroll
@@ -176,9 +191,8 @@ __global__ void prefix_kernel(Q35GqaPrefill p, int n_rows) {
         kf = q35_bf2f(p.kt[q35_k_index(g, pos, d, p.t_tiles)]);
         vf = q35_bf2f(p.vt[q35_v_index(g, pos, d, p.t_tiles)]);
     }
-    const int kb = pos >> 5, kr = pos & 31;
-    p.kw[(((size_t)g * p.kbt + kb) * 32 + kr) * D + d] = f16_bits(kf);
-    p.vw[(((size_t)g * p.kbt + kb) * D + d) * 32 + v_slot(kr)] = f16_bits(vf);
+    p.kw[kw_index(g, p.kbt, pos, d)] = f16_bits(kf);
+    p.vw[vw_index(g, p.kbt, pos >> 5, d, v_slot(pos & 31))] = f16_bits(vf);
 }
 
 /* q workspace rows [B, 16*nqb) of the last block: zeros */
@@ -194,26 +208,29 @@ __global__ void qpad_kernel(Q35GqaPrefill p, int n_pad) {
 
 
 
-/* LDS tiles of one 32-key block.  Rows are padded by one 16-byte granule
- * so the MFMA operand reads are conflict-free and take one address
- * register plus immediate offsets:
- *   K tile: 32 key rows x 33 granules (528 B; granule 32 unused),
- *   V tile: 256 dim rows x 5 granules (80 B; granule 4 unused). */
-constexpr int KROW = 33, VROW = 5;
-constexpr int KTILE = 32 * KROW * 8, VTILE = D * VROW * 8;      /* halfs */
+/* LDS: per group, two stages of one 32-key block, each the K tile (16 KB,
+ * granule-major as in the workspace) followed by the V tile (16 KB, rows
+ * swizzled as in the workspace).  A stage is a verbatim copy of the two
+ * workspace tiles: 32 direct-to-LDS loads of 1 KB (lane l -> bytes 16l..
+ * of the block), 8 per wave. */
+constexpr int TILE_HALFS = 32 * D;                               /* one K or V tile */
+constexpr int STAGE = 2 * TILE_HALFS;                            /* halfs a stage */
+constexpr uint32_t TILE_BYTES = TILE_HALFS * 2;
+static_assert(4 * STAGE * 2 == 8 * 16 * 64 * 4 * 4, "the merge area is the four stages");
 
-/* Instruction order for a block of 16 MFMAs fed by 16 LDS fragment reads:
- * 8 reads, then (4 MFMAs, 4 reads) x 3, then 4 MFMAs, so a batch of reads
- * is always in flight under the previous batch's MFMAs.  Left to itself
- * the scheduler minimises registers and waits on each read. */
+/* Instruction order for 16 MFMAs fed by 16 LDS fragment reads: READS reads
+ * ahead, then (READS MFMAs, READS reads) repeated, then the last MFMAs, so
+ * a batch of reads is always in flight under the previous batch's MFMAs.
+ * Left to itself the scheduler minimises registers and waits on each read. */
+template <int READS>
 __device__ __forceinline__ void sched_reads_ahead() {
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    /* DS reads */
+    __builtin_amdgcn_sched_group_barrier(0x100, READS, 0);   /* DS reads */
 #pragma unroll
-    for (int i = 0; i < 3; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  /* MFMA */
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    for (int i = 0; i < 16 / READS - 1; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, READS, 0);  /* MFMA */
+        __builtin_amdgcn_sched_group_barrier(0x100, READS, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, READS, 0);
 }
 
 /* max of v over the two 32-lane halves (lanes l and l ^ 32), on the
@@ -223,133 +240,188 @@ __device__ __forceinline__ float half_pair_max(float v) {
     return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
 }
 
-/* Causal work per q block grows with its position, so workgroup x runs
- * the pair of q blocks (nqb-1-x, x): the longest with the shortest, equal
- * total work for every workgroup whatever CU it lands on. */
-__global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
-    const int g = blockIdx.y;
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int h = lane >> 5, col = lane & 31;
-    const int hl = 2 * w + (col >> 4);
-    const int end = p.t0 + p.B;
+/* s_waitcnt vmcnt(0) (expcnt and lgkmcnt left open): this wave's direct-to-
+ * LDS loads have landed */
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-    __shared__ __align__(16) _Float16 sK[2][KTILE];
-    __shared__ __align__(16) _Float16 sV[2][VTILE];
+/* One direct-to-LDS load: 16 bytes a lane from buffer offset soff + voff
+ * (range-checked) to LDS byte lds + 16 * lane.  Issued as inline assembly
+ * so the compiler's wait insertion does not see it: it cannot tell LDS
+ * stages apart and would wait for every staging load in flight before the
+ * next LDS read.  The kernel orders these loads itself (wait_dma() before
+ * each barrier); loads the compiler does not count can only make its own
+ * load waits stricter. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   /* m0 is reserved; nothing else here uses it */
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff,
+                                      uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
-    /* staging: thread t moves granules t + 256 j (j < 4) of the K tile
-     * (row (t + 256 j) / 32) and of the V tile (row (t + 256 j) / 4) through
-     * registers.  Buffer loads on a range-checked resource per kv head: the
-     * tile offset is the scalar offset, the lane's offset a loop-invariant
-     * VGPR. */
-    const uint32_t tile_bytes = 32 * D * 2;
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t *>(p.kw + (size_t)g * p.kbt * 32 * D), 0, p.kbt * tile_bytes, Q35_BUF_DW3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t *>(p.vw + (size_t)g * p.kbt * D * 32), 0, p.kbt * tile_bytes, Q35_BUF_DW3);
-    uint32_t kgo[4], vgo[4];
-    int klo[4], vlo[4];
+/* q block qb's output rows of this wave: O / l times sigmoid(gate), fp32 */
+__device__ __forceinline__ void store_rows(const Q35GqaPrefill &p, int g, int qb, int hl, int col,
+                                           int h, float l_run, const f32x16_t (&acc)[8]) {
+    const int end = p.t0 + p.B, qpos = p.t0 + 16 * qb + (col & 15);
+    const float L = l_run + __shfl_xor(l_run, 32);
+    if (qpos >= end) return;
+    const int b = qpos - p.t0, head = g * G + hl;
+    const float *gate = p.q_gate + ((size_t)b * p.heads + head) * 2 * D + D;
+    float *out = p.attn_out + ((size_t)b * p.heads + head) * D;
+    const float inv = 1.0f / L;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int gi = t + 256 * j;
-        kgo[j] = (uint32_t)gi * 16u;                 /* K tile: 32 granules a row */
-        vgo[j] = (uint32_t)gi * 16u;                 /* V tile: 4 granules a row */
-        klo[j] = ((gi >> 5) * KROW + (gi & 31)) * 8;
-        vlo[j] = ((gi >> 2) * VROW + (gi & 3)) * 8;
+    for (int dt = 0; dt < 8; dt++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = 32 * dt + 8 * j + 4 * h;
+            const float4 gv = *reinterpret_cast<const float4 *>(gate + d);
+            float4 o;
+            o.x = acc[dt][4 * j + 0] * inv * q35_sigmoid(gv.x);
+            o.y = acc[dt][4 * j + 1] * inv * q35_sigmoid(gv.y);
+            o.z = acc[dt][4 * j + 2] * inv * q35_sigmoid(gv.z);
+            o.w = acc[dt][4 * j + 3] * inv * q35_sigmoid(gv.w);
+            *reinterpret_cast<float4 *>(out + d) = o;
+        }
     }
-    const int kbase = (col * KROW + h) * 8;          /* + 16 ks halfs */
-    const int vbase = (col * VROW + h) * 8;          /* + dt * 32 rows + 16 ks halfs */
+}
 
-  for (int item = 0; item < 2; item++) {
-    const int qb = item == 0 ? p.nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    if (item == 1 && qb >= p.nqb - 1 - (int)blockIdx.x) break;   /* odd middle block */
-    const int q0 = p.t0 + 16 * qb;
-    const int qpos = q0 + (col & 15);
-    const int n_keys = min(q0 + 16, end);
-    const int nkb = (n_keys + 31) >> 5;
-
-    /* Q^T as the B operand for the wave's 32 columns, all 16 k-steps */
+/* Q^T of q block qb as the B operand for the wave's 32 columns, all 16
+ * k-steps */
+__device__ __forceinline__ void load_q(const Q35GqaPrefill &p, int g, int qb, int hl, int col, int h,
+                                       f16x8_t (&qop)[16]) {
     const uint16_t *qrow = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + (col & 15)) * D;
-    f16x8_t qop[16];
 #pragma unroll
     for (int ks = 0; ks < 16; ks++)
         qop[ks] = *reinterpret_cast<const f16x8_t *>(qrow + 16 * ks + 8 * h);
+}
 
-    f32x16_t acc[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc[dt][i] = 0.0f;
-    float m_used = -INFINITY, l_run = 0.0f;
+/* Causal work per q block grows with its position.  Workgroup x serves a
+ * long q block (nqb-1-x) and a short one (x) of one kv head with 8 waves in
+ * two groups of 4 (one wave of each group per SIMD).  Wave w of a group owns
+ * 32 query columns: heads 2w, 2w+1 of the kv head x the block's 16
+ * positions.  With nL and nS the blocks' 32-key tile counts, group A runs
+ * the long block's tiles [0, nA), nA = ceil((nL + nS) / 2); group B runs the
+ * short block's nS tiles, stores its rows, then the long block's tiles
+ * [nA, nL).  Both groups step through nA intervals between workgroup
+ * barriers, so every workgroup carries the same causal work.  At the end
+ * group B hands its partial (max, sum, O) of the long block to group A
+ * through LDS, and group A merges and stores the long block's rows.
+ * Per tile and wave:
+ *   S^T[32 key][32 q] = K Q^T   (16 x v_mfma_f32_32x32x16_f16),
+ *   online softmax per column (rescaled only when a column max grows by
+ *   more than 8 in scaled units, which keeps P <= e^8 in fp16),
+ *   O^T[256][32 q] += V^T P^T  (16 x 32x32x16 f16; the S^T accumulator
+ *   registers are P's B operand as they stand, the value tile is stored in
+ *   the matching key order).
+ * The two waves of a SIMD run out of phase: in interval it group A does
+ * QK, softmax and PV of its tile it, while group B does softmax and PV of
+ * its tile it-1 and then QK of its tile it, so one wave's softmax (VALU)
+ * runs under the other's MFMAs.
+ * K / V tiles move global -> LDS by direct-to-LDS buffer loads into two
+ * stages per group, issued one interval ahead of use: for group A the K
+ * and V tiles of tile it+1; for group B the K tile of tile it+1 and the V
+ * tile of tile it (which it reads in the next interval), so no stage part
+ * is written in an interval in which its group reads it. */
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kernel(Q35GqaPrefill p) {
+    const int g = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int grp = w >> 2, wg = w & 3;
+    const int h = lane >> 5, col = lane & 31;
+    const int hl = 2 * wg + (col >> 4);
+    const int end = p.t0 + p.B;
 
-    /* tile 0 into stage 0, tile 1 into the staging registers; every load is
-     * unconditional (a tile index past the end is clamped and its copy is
-     * never read), so the compiler waits on exactly the loads it needs */
-    u32x4_t stg[8];
+    __shared__ __align__(16) _Float16 smem[4 * STAGE];   /* [group][stage] */
+    __shared__ float sml[4][2][64];                      /* group B's m, l */
+
+    const int x = blockIdx.x, qL = p.nqb - 1 - x, qS = x;
+    const bool has_short = qS < qL;
+    const int nL = (min(p.t0 + 16 * qL + 16, end) + 31) >> 5;
+    const int nS = has_short ? (min(p.t0 + 16 * qS + 16, end) + 31) >> 5 : 0;
+    const int nA = (nL + nS + 1) >> 1;          /* intervals, and group A's tiles */
+    const int nB = nS + nL - nA;                /* group B's tiles, nB <= nA */
+    /* group B's j-th tile and its q block */
+    auto tile_b = [&](int j) { return j < nS ? j : nA + j - nS; };
+    auto block_b = [&](int j) { return j < nS ? qS : qL; };
+
+    /* direct-to-LDS staging: this wave copies 1 KB blocks wg + 4i of a
+     * stage part (the K tile, then the V tile) */
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(p.kw + (size_t)g * p.kbt * TILE_HALFS)), 0,
+        p.kbt * TILE_BYTES, Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(p.vw + (size_t)g * p.kbt * TILE_HALFS)), 0,
+        p.kbt * TILE_BYTES, Q35_BUF_DW3);
+    const uint32_t dma_lane = (uint32_t)lane * 16;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) _Float16 *)smem;
+    auto stage_part = [&](int stage, int part, int tile) {
+        const uint32_t base = lds0 + (uint32_t)((grp * 2 + stage) * STAGE + part * TILE_HALFS) * 2;
+        const uint32_t so = (uint32_t)tile * TILE_BYTES;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        stg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, kgo[j], 0, 0);
-        stg[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vgo[j], 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        *reinterpret_cast<u32x4_t *>(&sK[0][klo[j]]) = stg[j];
-        *reinterpret_cast<u32x4_t *>(&sV[0][vlo[j]]) = stg[4 + j];
-    }
-    {
-        const uint32_t so = (uint32_t)min(1, nkb - 1) * tile_bytes;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            stg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, kgo[j], so, 0);
-            stg[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vgo[j], so, 0);
+        for (int i = 0; i < 4; i++) {
+            const int j = wg + 4 * i;
+            dma16(part ? vrs : krs, base + j * 1024, dma_lane, so + j * 1024);
         }
-    }
-    q35_lds_barrier();
+    };
 
-    for (int kb = 0; kb < nkb; kb++) {
-        const int buf = kb & 1;
-        /* S^T = K Q^T: lane holds column col, keys 32kb + 8j + 4h + i' */
-        f32x16_t s;
+    /* operand read addresses: K granule 2ks + h of key col at
+     * (2ks + h) * 32 + col; V row 32dt + col, granule h + 2(u & 1) (swizzled) */
+    const int kbase = (h * 32 + col) * 8;                             /* + 512 ks halfs */
+    const int vsw = (col >> 2) & 3;
+    const int vb0 = TILE_HALFS + col * 32 + ((h ^ vsw) << 3);         /* + 1024 dt halfs */
+    const int vb1 = TILE_HALFS + col * 32 + (((h + 2) ^ vsw) << 3);
+
+    f16x8_t qop[16];
+    f32x16_t acc[8];
+    float m_used, l_run;
+    auto reset = [&]() {
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[dt][i] = 0.0f;
+        m_used = -INFINITY;
+        l_run = 0.0f;
+    };
+
+    /* S^T = K Q^T: lane holds column col, keys 32kb + 8j + 4h + i' */
+    auto qk = [&](int stage, f32x16_t &s) {
+        const _Float16 *sb = smem + (grp * 2 + stage) * STAGE;
 #pragma unroll
         for (int i = 0; i < 16; i++) s[i] = 0.0f;
-        {
-            const _Float16 *kp = &sK[buf][kbase];
-            f16x8_t ka[2][4];
+        f16x8_t ka[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++) ka[0][u] = *reinterpret_cast<const f16x8_t *>(kp + 16 * u);
+        for (int ks = 0; ks < 16; ks++) ka[ks] = *reinterpret_cast<const f16x8_t *>(sb + kbase + 512 * ks);
 #pragma unroll
-            for (int bq = 0; bq < 4; bq++) {
-                if (bq < 3) {
-#pragma unroll
-                    for (int u = 0; u < 4; u++)
-                        ka[(bq + 1) & 1][u] =
-                            *reinterpret_cast<const f16x8_t *>(kp + 16 * (4 * (bq + 1) + u));
-                }
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-                    s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[bq & 1][u], qop[4 * bq + u], s, 0, 0, 0);
-            }
-            sched_reads_ahead();
-        }
+        for (int ks = 0; ks < 16; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qop[ks], s, 0, 0, 0);
+        sched_reads_ahead<4>();
+    };
+
+    /* online softmax of tile kb of q block qb, then O^T += V^T P^T */
+    auto softmax_pv = [&](int stage, f32x16_t &s, int kb, int qb) {
         /* element i is key 32kb + 8(i/4) + 4h + i%4: causal (key <= qpos) and
          * inside the batch (key < end) as one per-lane bound on the
-         * compile-time offset 8(i/4) + i%4.  Scores stay unscaled here; the
-         * 1/16 scale rides in the exponent's multiplier. */
-        const int lim = min(qpos + 1, end) - 32 * kb - 4 * h;
-        float mx = -INFINITY;
+         * compile-time offset 8(i/4) + i%4, applied only on a tile that
+         * reaches past the block's first position or the batch end.  Scores
+         * stay unscaled here; the 1/16 scale rides in the exponent's
+         * multiplier. */
+        const int q0 = p.t0 + 16 * qb;
+        if (32 * kb + 32 > min(q0 + 1, end)) {
+            const int lim = min(q0 + (col & 15) + 1, end) - 32 * kb - 4 * h;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float v = (8 * (i >> 2) + (i & 3)) < lim ? s[i] : -INFINITY;
-            s[i] = v;
-            mx = fmaxf(mx, v);
+            for (int i = 0; i < 16; i++) s[i] = (8 * (i >> 2) + (i & 3)) < lim ? s[i] : -INFINITY;
         }
+        float mx = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++) mx = fmaxf(mx, s[i]);
         mx = half_pair_max(mx);
         const bool need = mx > m_used + RESCALE_MARGIN / SCALE;
         if (__any(need)) {
             const float m_new = need ? mx : m_used;
             const float alpha = exp2f_fast((m_used - m_new) * EXP_K);   /* -inf -> 0 on first use */
             l_run *= alpha;
-            /* one 16-register tile at a time: the accumulators live in
-             * AGPRs and this rare path must not hold all 128 in VGPRs */
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 acc[dt] *= alpha;
@@ -358,82 +430,108 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(Q35GqaPrefill p) {
             m_used = m_new;
         }
         f16x8_t pb[2];
-        float ps = 0.0f;
         const float mk = m_used * EXP_K;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float pv = exp2f_fast(fmaf(s[i], EXP_K, -mk));
-            ps += pv;
-            pb[i >> 3][i & 7] = (_Float16)pv;
+        for (int i = 0; i < 16; i++) pb[i >> 3][i & 7] = (_Float16)exp2f_fast(fmaf(s[i], EXP_K, -mk));
+        /* the row sum of the fp16 weights the PV product uses, two a step */
+        float ps = 0.0f;
+        const f16x2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f16x2_t pr = {pb[i >> 2][2 * (i & 3)], pb[i >> 2][2 * (i & 3) + 1]};
+            ps = __builtin_amdgcn_fdot2(pr, one2, ps, false);
         }
         l_run += ps;
-        /* O^T += V^T P^T, V fragments in batches of 4 (two dim tiles) */
-        {
-            const _Float16 *vp = &sV[buf][vbase];
-            f16x8_t va[2][4];
+        const _Float16 *sb = smem + (grp * 2 + stage) * STAGE;
+        f16x8_t va[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                va[0][u] = *reinterpret_cast<const f16x8_t *>(vp + (u >> 1) * 32 * VROW * 8 + 16 * (u & 1));
+        for (int u = 0; u < 16; u++)
+            va[u] = *reinterpret_cast<const f16x8_t *>(sb + ((u & 1) ? vb1 : vb0) + 1024 * (u >> 1));
 #pragma unroll
-            for (int bq = 0; bq < 4; bq++) {
-                if (bq < 3) {
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int dt = 2 * (bq + 1) + (u >> 1);
-                        va[(bq + 1) & 1][u] =
-                            *reinterpret_cast<const f16x8_t *>(vp + dt * 32 * VROW * 8 + 16 * (u & 1));
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const int dt = 2 * bq + (u >> 1);
-                    acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[bq & 1][u], pb[u & 1], acc[dt],
-                                                                     0, 0, 0);
-                }
-            }
-            sched_reads_ahead();
-        }
-        /* staged tile kb+1 into the other stage (every wave finished tile
-         * kb-1, its previous occupant, before the last barrier), then the
-         * loads of tile kb+2 */
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            *reinterpret_cast<u32x4_t *>(&sK[buf ^ 1][klo[j]]) = stg[j];
-            *reinterpret_cast<u32x4_t *>(&sV[buf ^ 1][vlo[j]]) = stg[4 + j];
-        }
-        {
-            const uint32_t so = (uint32_t)min(kb + 2, nkb - 1) * tile_bytes;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                stg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, kgo[j], so, 0);
-                stg[4 + j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vgo[j], so, 0);
-            }
-        }
+        for (int u = 0; u < 16; u++)
+            acc[u >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[u], pb[u & 1], acc[u >> 1], 0, 0, 0);
+        sched_reads_ahead<4>();
+    };
+
+    reset();
+    f32x16_t s;
+    if (grp == 0) {
+        load_q(p, g, qL, hl, col, h, qop);
+        stage_part(0, 0, 0);
+        stage_part(0, 1, 0);
+        wait_dma();
         q35_lds_barrier();
+        for (int it = 0; it < nA; it++) {
+            /* the next tile's K, then its V, each as a burst of four
+             * loads ahead of the phase that follows */
+            if (it + 1 < nA) stage_part((it + 1) & 1, 0, it + 1);
+            qk(it & 1, s);
+            if (it + 1 < nA) stage_part((it + 1) & 1, 1, it + 1);
+            softmax_pv(it & 1, s, it, qL);
+            wait_dma();
+            q35_lds_barrier();
+        }
+    } else {
+        if (nB > 0) {
+            load_q(p, g, block_b(0), hl, col, h, qop);
+            stage_part(0, 0, tile_b(0));
+        }
+        wait_dma();
+        q35_lds_barrier();
+        for (int it = 0; it < nA; it++) {
+            if (it < nB) stage_part(it & 1, 1, tile_b(it));
+            if (it >= 1 && it <= nB) {
+                softmax_pv((it - 1) & 1, s, tile_b(it - 1), block_b(it - 1));
+                if (it == nS && it < nB) {
+                    /* the short block is done: its rows out, the long
+                     * block's tail next */
+                    store_rows(p, g, qS, hl, col, h, l_run, acc);
+                    reset();
+                    load_q(p, g, qL, hl, col, h, qop);
+                    /* all of this wave's loads done: the compiler then
+                     * places no load-count waits for q on the common
+                     * path, where they would also wait for staging loads */
+                    wait_dma();
+                }
+            }
+            if (it + 1 < nB) stage_part((it + 1) & 1, 0, tile_b(it + 1));
+            if (it < nB) qk(it & 1, s);
+            wait_dma();
+            q35_lds_barrier();
+        }
+        if (nB == nA && nB > 0) softmax_pv((nB - 1) & 1, s, tile_b(nB - 1), block_b(nB - 1));
     }
 
-    const float L = l_run + __shfl_xor(l_run, 32);
-    if (qpos < end) {
-        const int b = qpos - p.t0, head = g * G + hl;
-        const float *gate = p.q_gate + ((size_t)b * p.heads + head) * 2 * D + D;
-        float *out = p.attn_out + ((size_t)b * p.heads + head) * D;
-        const float inv = 1.0f / L;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int d = 32 * dt + 8 * j + 4 * h;
-                const float4 gv = *reinterpret_cast<const float4 *>(gate + d);
-                float4 o;
-                o.x = acc[dt][4 * j + 0] * inv * q35_sigmoid(gv.x);
-                o.y = acc[dt][4 * j + 1] * inv * q35_sigmoid(gv.y);
-                o.z = acc[dt][4 * j + 2] * inv * q35_sigmoid(gv.z);
-                o.w = acc[dt][4 * j + 3] * inv * q35_sigmoid(gv.w);
-                *reinterpret_cast<float4 *>(out + d) = o;
-            }
+    /* group B's partial of the long block -> LDS -> group A; the stages are
+     * idle after the last barrier.  When group B has no long tiles
+     * (nB = nS), its rows are the short block's, and it hands over an
+     * empty partial. */
+    q35_lds_barrier();
+    float *mrg = reinterpret_cast<float *>(smem) + wg * 128 * 64 + lane;
+    if (grp == 1) {
+        if (nS > 0 && nB == nS) {
+            store_rows(p, g, qS, hl, col, h, l_run, acc);
+            m_used = -INFINITY;
         }
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) mrg[(16 * dt + i) * 64] = acc[dt][i];
+        sml[wg][0][lane] = m_used;
+        sml[wg][1][lane] = l_run;
     }
-  }
+    q35_lds_barrier();
+    if (grp == 0) {
+        const float mB = sml[wg][0][lane], lB = sml[wg][1][lane];
+        const float M = fmaxf(m_used, mB);
+        const float fa = exp2f_fast((m_used - M) * EXP_K);
+        const float fb = mB == -INFINITY ? 0.0f : exp2f_fast((mB - M) * EXP_K);
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[dt][i] = acc[dt][i] * fa + mrg[(16 * dt + i) * 64] * fb;
+        store_rows(p, g, qL, hl, col, h, l_run * fa + lB * fb, acc);
+    }
 }
 
 }  // namespace
@@ -476,6 +574,6 @@ extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stre
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(attn_kernel, dim3((p.nqb + 1) / 2, p.kv_heads), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(attn_kernel, dim3((p.nqb + 1) / 2, p.kv_heads), dim3(512), 0, stream, p);
     return hipGetLastError();
 }
