@@ -50,6 +50,12 @@ static struct Plugin {
     size_t d_stage_cap, h_stage_cap;
     void *d_ws;                /* prefill workspaces (grow-only) */
     size_t ws_cap;
+
+    /* whole-layer steps: per-layer device weights, the activations between
+     * their launches, a device copy of the host state */
+    int hidden;
+    struct LayerW *lw;         /* [n_layers] */
+    float *d_act, *d_state;
 } P;
 
 static void set_err(const char *fmt, ...) {
@@ -62,6 +68,7 @@ static void set_err(const char *fmt, ...) {
 const char *ds4f_gpu_last_error(void) { return P.err; }
 
 static void mlx4_free(void);
+static void layers_free(void);
 
 #define HIPCHK(call)                                                              \
     do {                                                                          \
@@ -102,6 +109,7 @@ int ds4f_gpu_init(void) {
 }
 
 static void free_binding(void) {
+    layers_free();
     if (P.d_k) hipFree(P.d_k);
     if (P.d_v) hipFree(P.d_v);
     if (P.d_lin) hipFree(P.d_lin);
@@ -800,7 +808,7 @@ int ds4f_gpu_mlx4_matvec(const uint32_t *vals, const uint16_t *scales, const uin
     if (mlx4_stage((size_t)C, (size_t)R, 0) != 0) return -1;
     memcpy(M.h_x, x, (size_t)C * sizeof(float));
     HIPCHK(hipMemcpyAsync(M.d_x, M.h_x, (size_t)C * sizeof(float), hipMemcpyHostToDevice, P.stream));
-    Q35Mlx4 p = {mlx4_v(&M.head), mlx4_s(&M.head), mlx4_b(&M.head), M.d_x, M.d_y, NULL, R, C};
+    Q35Mlx4 p = {mlx4_v(&M.head), mlx4_s(&M.head), mlx4_b(&M.head), M.d_x, M.d_y, NULL, R, C, NULL, 0};
     HIPCHK(q35_mlx4_matvec(&p, 1, P.stream));
     HIPCHK(hipMemcpyAsync(M.h_y, M.d_y, (size_t)R * sizeof(float), hipMemcpyDeviceToHost, P.stream));
     HIPCHK(hipStreamSynchronize(P.stream));
@@ -837,14 +845,14 @@ int ds4f_gpu_mlx4_batch(const uint32_t *const *vals, const uint16_t *const *scal
             return -1;
         memcpy(M.h_x + (size_t)j * C, xs[j], (size_t)C * sizeof(float));
         const Q35Mlx4Job jb = {mlx4_v(&M.slot[i]), mlx4_s(&M.slot[i]), mlx4_b(&M.slot[i]),
-                               M.d_x + (size_t)j * C, M.d_y + (size_t)j * R};
+                               M.d_x + (size_t)j * C, M.d_y + (size_t)j * R, R};
         M.h_jobs[j] = jb;
     }
     HIPCHK(hipMemcpyAsync(M.d_x, M.h_x, (size_t)njobs * C * sizeof(float), hipMemcpyHostToDevice,
                           P.stream));
     HIPCHK(hipMemcpyAsync(M.d_jobs, M.h_jobs, (size_t)njobs * sizeof(Q35Mlx4Job),
                           hipMemcpyHostToDevice, P.stream));
-    Q35Mlx4 p = {NULL, NULL, NULL, NULL, NULL, M.d_jobs, R, C};
+    Q35Mlx4 p = {NULL, NULL, NULL, NULL, NULL, M.d_jobs, R, C, NULL, 0};
     HIPCHK(q35_mlx4_matvec(&p, njobs, P.stream));
     HIPCHK(hipMemcpyAsync(M.h_y, M.d_y, (size_t)njobs * R * sizeof(float), hipMemcpyDeviceToHost,
                           P.stream));
@@ -857,7 +865,278 @@ int ds4f_hip_mlx4_matvec_async(const uint32_t *vals, const uint16_t *scales,
                                const uint16_t *biases, int R, int C, const float *x, float *y,
                                void *stream) {
     if (mlx4_ready(R, C) != 0) return -1;
-    Q35Mlx4 p = {vals, scales, biases, x, y, NULL, R, C};
+    Q35Mlx4 p = {vals, scales, biases, x, y, NULL, R, C, NULL, 0};
     HIPCHK(q35_mlx4_matvec(&p, 1, pick(stream)));
     return 0;
 }
+
+/* ---- whole attention layers (src/attn_qwen.c:87-225, :837-968) ---------- */
+
+typedef struct LayerW {
+    void *d;                   /* one allocation holding every tensor below */
+    const uint16_t *in_norm;   /* input_layernorm, or NULL */
+    Q35Mlx4Job *jobs;          /* projections of xin (x NULL: the launch's x) */
+    int njobs, rmax;
+    Q35Mlx4 out;               /* output projection: x, y set per call */
+    const uint16_t *qn, *kn, *conv_w, *dt_bias, *norm_w;
+    const float *A_log;
+} LayerW;
+
+/* activations between the launches of one layer step, floats */
+enum { ACT_Q, ACT_K, ACT_V, ACT_AO, ACT_QKV, ACT_Z, ACT_A, ACT_B, ACT_LO, ACT_N };
+
+static size_t act_len(int i) {
+    const size_t H = (size_t)P.g.n_heads, KVH = (size_t)P.g.n_kv_heads;
+    switch (i) {
+    case ACT_Q: return H * 2 * GQA_D;
+    case ACT_K: case ACT_V: return KVH * GQA_D;
+    case ACT_AO: return H * GQA_D;
+    case ACT_QKV: return (size_t)P.rows;
+    case ACT_Z: case ACT_LO: return (size_t)P.vh * P.vd;
+    default: return (size_t)P.vh;          /* a, b */
+    }
+}
+
+static float *act(int i) {
+    size_t off = 0;
+    for (int j = 0; j < i; j++) off += (act_len(j) + 63) & ~(size_t)63;
+    return P.d_act + off;
+}
+
+static void layers_free(void) {
+    if (P.lw) {
+        for (int l = 0; l < P.g.n_layers; l++)
+            if (P.lw[l].d) hipFree(P.lw[l].d);
+        free(P.lw);
+    }
+    if (P.d_act) hipFree(P.d_act);
+    if (P.d_state) hipFree(P.d_state);
+    P.lw = NULL;
+    P.d_act = P.d_state = NULL;
+    P.hidden = 0;
+}
+
+static int mlx4_shape_ok(const Ds4fGpuMlx4W *m, int rows, int cols, const char *name) {
+    if (!m->vals || !m->scales || m->rows != rows || m->cols != cols ||
+        !q35_mlx4_supported(rows, cols)) {
+        set_err("layer weights: %s is %dx%d, expected %dx%d", name, m->rows, m->cols, rows, cols);
+        return 0;
+    }
+    return 1;
+}
+
+/* tensors of a layer in one allocation: every part with bytes > 0 gets a
+ * 256-byte aligned slot (its device address in *dst, else NULL) and is
+ * copied when it has a host source */
+typedef struct { const void *src; size_t bytes; const void **dst; } Part;
+
+static int upload_parts(LayerW *lw, Part *pt, int n) {
+    size_t total = 0;
+    for (int i = 0; i < n; i++) total += (pt[i].bytes + 255) & ~(size_t)255;
+    HIPCHK(hipMalloc(&lw->d, total));
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        char *d = (char *)lw->d + off;
+        *pt[i].dst = pt[i].bytes ? d : NULL;
+        if (pt[i].src && pt[i].bytes) HIPCHK(hipMemcpy(d, pt[i].src, pt[i].bytes, hipMemcpyHostToDevice));
+        off += (pt[i].bytes + 255) & ~(size_t)255;
+    }
+    return 0;
+}
+
+/* the parts of one MLX 4-bit weight: vals, scales, biases */
+static int mlx4_parts(Part *pt, const Ds4fGpuMlx4W *m, const void **v, const void **sc,
+                      const void **b) {
+    const size_t n = (size_t)m->rows * m->cols, ng = (n + 63) / 64;
+    pt[0] = (Part){m->vals, n / 2, v};
+    pt[1] = (Part){m->scales, ng * 2, sc};
+    pt[2] = (Part){m->biases, m->biases ? ng * 2 : 0, b};
+    return 3;
+}
+
+int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers || !w) return -1;
+    const int kind = P.kind[L];
+    if (kind != DS4F_LAYER_GQA && kind != DS4F_LAYER_LINEAR) {
+        set_err("layer %d has no attention kind", L);
+        return -1;
+    }
+    const int hidden = kind == DS4F_LAYER_GQA ? w->q.cols : w->qkv.cols;
+    if (P.hidden && hidden != P.hidden) {
+        set_err("layer weights: hidden %d differs from %d", hidden, P.hidden);
+        return -1;
+    }
+    const int H = P.g.n_heads, KVH = P.g.n_kv_heads;
+    if (kind == DS4F_LAYER_GQA) {
+        if (!mlx4_shape_ok(&w->q, H * 2 * GQA_D, hidden, "q_proj") ||
+            !mlx4_shape_ok(&w->k, KVH * GQA_D, hidden, "k_proj") ||
+            !mlx4_shape_ok(&w->v, KVH * GQA_D, hidden, "v_proj") ||
+            !mlx4_shape_ok(&w->o, hidden, H * GQA_D, "o_proj") || !w->q_norm || !w->k_norm)
+            return -1;
+    } else {
+        if (!mlx4_shape_ok(&w->qkv, P.rows, hidden, "in_proj_qkv") ||
+            !mlx4_shape_ok(&w->z, P.vh * P.vd, hidden, "in_proj_z") ||
+            !mlx4_shape_ok(&w->a, P.vh, hidden, "in_proj_a") ||
+            !mlx4_shape_ok(&w->b, P.vh, hidden, "in_proj_b") ||
+            !mlx4_shape_ok(&w->out, hidden, P.vh * P.vd, "out_proj") || !w->conv_w ||
+            !w->A_log || !w->dt_bias || !w->norm_w)
+            return -1;
+    }
+    if (!P.lw) {
+        P.lw = (LayerW *)calloc((size_t)P.g.n_layers, sizeof(LayerW));
+        if (!P.lw) return -1;
+    }
+    if (!P.d_act) {
+        size_t n = 0;
+        for (int i = 0; i < ACT_N; i++) n += (act_len(i) + 63) & ~(size_t)63;
+        HIPCHK(hipMalloc((void **)&P.d_act, n * sizeof(float)));
+        HIPCHK(hipMalloc((void **)&P.d_state, (size_t)hidden * sizeof(float)));
+    }
+    P.hidden = hidden;
+    LayerW *lw = &P.lw[L];
+    if (lw->d) {
+        HIPCHK(hipStreamSynchronize(P.stream));
+        hipFree(lw->d);
+    }
+    memset(lw, 0, sizeof *lw);
+
+    const Ds4fGpuMlx4W *proj[4], *outw;
+    int np = 0, yact[4];
+    if (kind == DS4F_LAYER_GQA) {
+        proj[0] = &w->q, proj[1] = &w->k, proj[2] = &w->v;
+        yact[0] = ACT_Q, yact[1] = ACT_K, yact[2] = ACT_V;
+        np = 3;
+        outw = &w->o;
+    } else {
+        proj[0] = &w->qkv, proj[1] = &w->z, proj[2] = &w->a, proj[3] = &w->b;
+        yact[0] = ACT_QKV, yact[1] = ACT_Z, yact[2] = ACT_A, yact[3] = ACT_B;
+        np = 4;
+        outw = &w->out;
+    }
+    Part pt[32];
+    const void *pv[5], *ps[5], *pb[5], *in_norm, *jobs, *t0, *t1, *t2, *t3;
+    int n = 0;
+    for (int i = 0; i < np; i++) n += mlx4_parts(pt + n, proj[i], &pv[i], &ps[i], &pb[i]);
+    n += mlx4_parts(pt + n, outw, &pv[4], &ps[4], &pb[4]);
+    pt[n++] = (Part){w->in_norm, w->in_norm ? (size_t)hidden * 2 : 0, &in_norm};
+    pt[n++] = (Part){NULL, (size_t)np * sizeof(Q35Mlx4Job), &jobs};   /* filled below */
+    if (kind == DS4F_LAYER_GQA) {
+        pt[n++] = (Part){w->q_norm, GQA_D * 2, &t0};
+        pt[n++] = (Part){w->k_norm, GQA_D * 2, &t1};
+    } else {
+        pt[n++] = (Part){w->conv_w, (size_t)P.rows * 4 * 2, &t0};
+        pt[n++] = (Part){w->A_log, (size_t)P.vh * 4, &t1};
+        pt[n++] = (Part){w->dt_bias, (size_t)P.vh * 2, &t2};
+        pt[n++] = (Part){w->norm_w, (size_t)P.vd * 2, &t3};
+    }
+    if (upload_parts(lw, pt, n) != 0) {
+        if (lw->d) hipFree(lw->d);
+        memset(lw, 0, sizeof *lw);
+        return -1;
+    }
+    /* the projections' job table, pointing at the weights just placed */
+    Q35Mlx4Job hj[4];
+    lw->rmax = 0;
+    for (int i = 0; i < np; i++) {
+        hj[i] = (Q35Mlx4Job){(const uint32_t *)pv[i], (const uint16_t *)ps[i],
+                             (const uint16_t *)pb[i], NULL, act(yact[i]), proj[i]->rows};
+        if (proj[i]->rows > lw->rmax) lw->rmax = proj[i]->rows;
+    }
+    if (hipMemcpy((void *)jobs, hj, (size_t)np * sizeof(Q35Mlx4Job), hipMemcpyHostToDevice) !=
+        hipSuccess) {
+        set_err("layer weights: job table upload failed");
+        hipFree(lw->d);
+        memset(lw, 0, sizeof *lw);
+        return -1;
+    }
+    lw->jobs = (Q35Mlx4Job *)jobs;
+    lw->njobs = np;
+    lw->in_norm = (const uint16_t *)in_norm;
+    memset(&lw->out, 0, sizeof lw->out);
+    lw->out.vals = (const uint32_t *)pv[4];
+    lw->out.scales = (const uint16_t *)ps[4];
+    lw->out.biases = (const uint16_t *)pb[4];
+    lw->out.R = outw->rows;
+    lw->out.C = outw->cols;
+    lw->out.accumulate = 1;
+    if (kind == DS4F_LAYER_GQA) {
+        lw->qn = (const uint16_t *)t0;
+        lw->kn = (const uint16_t *)t1;
+    } else {
+        lw->conv_w = (const uint16_t *)t0;
+        lw->A_log = (const float *)t1;
+        lw->dt_bias = (const uint16_t *)t2;
+        lw->norm_w = (const uint16_t *)t3;
+    }
+    return 0;
+}
+
+int ds4f_hip_attn_step_async(int L, int token, float *state, void *stream) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers) return -1;
+    const int kind = P.kind[L];
+    if (kind == DS4F_LAYER_NONE) return 0;                 /* src/attn_qwen.c:1264 */
+    if (!P.lw || !P.lw[L].d) {
+        set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
+        return -1;
+    }
+    if (token < 0 || token >= P.g.max_tokens) return 0;    /* :117, :882 */
+    const LayerW *lw = &P.lw[L];
+    hipStream_t st = pick(stream);
+    Q35Mlx4 pr;
+    memset(&pr, 0, sizeof pr);
+    pr.jobs = lw->jobs;
+    pr.R = lw->rmax;
+    pr.C = P.hidden;
+    pr.x = state;
+    pr.x_norm = lw->in_norm;
+    HIPCHK(q35_mlx4_matvec(&pr, lw->njobs, st));
+    Q35Mlx4 po = lw->out;
+    po.y = state;
+    if (kind == DS4F_LAYER_GQA) {
+        if (ds4f_hip_gqa_decode_async(L, token, act(ACT_Q), act(ACT_K), act(ACT_V), lw->qn,
+                                      lw->kn, act(ACT_AO), NULL, st) != 0)
+            return -1;
+        po.x = act(ACT_AO);
+    } else {
+        if (ds4f_hip_lin_decode_async(L, token, act(ACT_QKV), act(ACT_Z), act(ACT_A),
+                                      act(ACT_B), lw->conv_w, lw->A_log, lw->dt_bias, lw->norm_w,
+                                      act(ACT_LO), NULL, st) != 0)
+            return -1;
+        po.x = act(ACT_LO);
+    }
+    HIPCHK(q35_mlx4_matvec(&po, 1, st));
+    return 0;
+}
+
+int ds4f_gpu_attn_step(int L, int token, float *state) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers) return -1;
+    if (P.kind[L] == DS4F_LAYER_NONE || token < 0 || token >= P.g.max_tokens) return 0;
+    if (!P.lw || !P.lw[L].d) {
+        set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
+        return -1;
+    }
+    if (forced_failure()) return fail_over(token);
+    const size_t bytes = (size_t)P.hidden * sizeof(float);
+    if (ensure_stage(0, bytes) != 0) return fail_over(token);
+    memcpy(P.h_stage, state, bytes);
+    if (hipMemcpyAsync(P.d_state, P.h_stage, bytes, hipMemcpyHostToDevice, P.stream) !=
+            hipSuccess ||
+        ds4f_hip_attn_step_async(L, token, P.d_state, NULL) != 0 ||
+        download(P.d_state, bytes) != 0)
+        return fail_over(token);
+    memcpy(state, P.h_stage, bytes);
+    return 0;
+}
+

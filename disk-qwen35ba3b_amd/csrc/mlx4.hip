@@ -19,6 +19,9 @@
  * q*s+b accumulation, a float32 rounding difference (gpu.h:13-18).
  * The row's partial sums meet in a DPP wave reduction.  HBM-bound: R*C/2
  * bytes of nibbles plus R*C/16 bytes of scales and biases per matvec.
+ * Fused around it for the attention layer steps: the input RMSNorm of x
+ * (every wave holds all of x, so it normalises its own copy) and the
+ * residual add into y.
  */
 #include "q35_device.h"
 #include "q35_launch.h"
@@ -34,6 +37,7 @@ struct Mlx4Job {
     const uint16_t *scales, *biases;
     const float *x;
     float *y;
+    int R;
 };
 
 /* 32 nibble products of one lane: 4 words, 8 nibbles each, against x[32].
@@ -70,32 +74,71 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
     Mlx4Job j;
     if (p.jobs) {
         const Q35Mlx4Job &d = p.jobs[blockIdx.y];
-        j = {d.vals, d.scales, d.biases, d.x, d.y};
+        j = {d.vals, d.scales, d.biases, d.x ? d.x : p.x, d.y, d.R ? d.R : p.R};
     } else {
-        j = {p.vals, p.scales, p.biases, p.x, p.y};
+        j = {p.vals, p.scales, p.biases, p.x, p.y, p.R};
     }
-    const int R = p.R, C = p.C, lane = threadIdx.x & 63;
+    const int R = j.R, C = p.C, lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (NT / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (NT / 64);
+    if (2 * wave >= R) return;     /* a shorter job of a batch: no rows here */
 
-    /* x of this lane's columns (scaled by the inverse fp8 nibble unit)
-     * and their plain sums, per chunk */
-    const float xsc = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
-    float xr[NCH][32], xs[NCH];
+    /* x of this lane's columns and, with x_norm, its RMSNorm: the square
+     * sum in double over the wave, r = sqrtf(mean + 1e-6), x / r * w with
+     * the reference's two roundings (src/attn_qwen.c:142-157) */
+    float xv[NCH][32];
     bool live[NCH];
 #pragma unroll
     for (int ch = 0; ch < NCH; ch++) {
         const int c0 = ch * CHUNK + 32 * lane;
         live[ch] = c0 < C;
-        float s = 0.0f;
 #pragma unroll
         for (int q = 0; q < 8; q++) {
             const float4 v = live[ch] ? *reinterpret_cast<const float4 *>(j.x + c0 + 4 * q)
                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-            xr[ch][4 * q] = v.x * xsc;
-            xr[ch][4 * q + 1] = v.y * xsc;
-            xr[ch][4 * q + 2] = v.z * xsc;
-            xr[ch][4 * q + 3] = v.w * xsc;
-            s += (v.x + v.y) + (v.z + v.w);
+            xv[ch][4 * q] = v.x;
+            xv[ch][4 * q + 1] = v.y;
+            xv[ch][4 * q + 2] = v.z;
+            xv[ch][4 * q + 3] = v.w;
+        }
+    }
+    if (p.x_norm) {
+        double ss = 0.0;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++)
+#pragma unroll
+            for (int e = 0; e < 32; e++) ss += (double)xv[ch][e] * xv[ch][e];
+        ss = q35_wave_sum(ss);
+        const float r = sqrtf((float)(ss / (double)C) + 1e-6f);
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++) {
+            const int c0 = ch * CHUNK + 32 * lane;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 wb = live[ch] ? *reinterpret_cast<const uint4 *>(p.x_norm + c0 + 8 * q)
+                                          : make_uint4(0, 0, 0, 0);
+                const uint32_t wv[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float w = q35_bf2f((uint16_t)(wv[e >> 1] >> (16 * (e & 1))));
+                    xv[ch][8 * q + e] = xv[ch][8 * q + e] / r * w;
+                }
+            }
+        }
+    }
+
+    /* x scaled by the inverse fp8 nibble unit, and its plain sums, per chunk */
+    const float xsc = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+    float xr[NCH][32], xs[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ch++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            xr[ch][4 * q] = xv[ch][4 * q] * xsc;
+            xr[ch][4 * q + 1] = xv[ch][4 * q + 1] * xsc;
+            xr[ch][4 * q + 2] = xv[ch][4 * q + 2] * xsc;
+            xr[ch][4 * q + 3] = xv[ch][4 * q + 3] * xsc;
+            s += (xv[ch][4 * q] + xv[ch][4 * q + 1]) + (xv[ch][4 * q + 2] + xv[ch][4 * q + 3]);
         }
         xs[ch] = s;
     }
@@ -134,7 +177,7 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const float t = q35_wave_sum(part[u]);
-            if (lane == 0 && r0 + u < R) j.y[r0 + u] = t;
+            if (lane == 0 && r0 + u < R) j.y[r0 + u] = p.accumulate ? j.y[r0 + u] + t : t;
         }
     }
 }

@@ -125,12 +125,19 @@ hipError_t q35_synth_conv(float *ring, int rows, int token, uint64_t seed, uint6
 /* ---- MLX 4-bit affine matvec (src/kernels.c:104-219) ---- *
  * y[R] = W[R x C] x, W as U32 nibble words + BF16 scale / bias per 64
  * elements (biases may be NULL).  One job: the inline pointers, jobs NULL.
- * Batched: jobs points to njobs device descriptors sharing R and C. */
+ * Batched: jobs points to njobs device descriptors sharing C; a job's R
+ * is its own when non-zero, else the launch's R (R is the largest), and a
+ * job's x is its own when non-NULL, else the launch's x.
+ * x_norm: when non-NULL, every job reads RMSNorm(x) with these BF16
+ * weights (the input_layernorm of src/attn_qwen.c:142-157: double sum of
+ * squares, eps 1e-6 on the mean, x / r * w) instead of x.  accumulate:
+ * y += W x (the residual add of :222, :833) instead of y = W x. */
 typedef struct Q35Mlx4Job {
     const uint32_t *vals;
     const uint16_t *scales, *biases;
     const float *x;
     float *y;
+    int R;
 } Q35Mlx4Job;
 typedef struct Q35Mlx4 {
     const uint32_t *vals;
@@ -139,6 +146,8 @@ typedef struct Q35Mlx4 {
     float *y;
     const Q35Mlx4Job *jobs;        /* device array, or NULL for the inline job */
     int R, C;
+    const uint16_t *x_norm;
+    int accumulate;
 } Q35Mlx4;
 /* 1 if the kernel takes this shape: C % 32 == 0, 32 <= C <= 8192 */
 int q35_mlx4_supported(int R, int C);

@@ -15,7 +15,7 @@ import ctypes
 import numpy as np
 
 from . import lib as _L
-from .workloads import GqaGeom, LinGeom, LinWeights
+from .workloads import GqaGeom, GqaLayerW, LinGeom, LinLayerW, LinWeights
 
 
 def _p(a):
@@ -114,6 +114,42 @@ class GpuAttention:
                                            _p(_u16(w.dt_bias)), _p(_u16(w.norm_w)), _p(out))
         _L.check(rc, "ds4f_gpu_lin_prefill")
         return out, qkv
+
+
+    # ---- whole layer steps (src/attn_qwen.c:87-225, :837-968) ----
+    def set_layer_weights(self, L: int, w: GqaLayerW | LinLayerW):
+        """Upload layer L's weights (ds4f_gpu_attn_weights)."""
+        keep = []
+
+        def arr(a, dt):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        def m4(m):
+            return _L.Mlx4W(arr(m.vals, np.uint32), arr(m.scales, np.uint16),
+                            arr(m.biases, np.uint16), m.rows, m.cols)
+
+        lw = _L.LayerW()
+        lw.in_norm = arr(w.in_norm, np.uint16)
+        if isinstance(w, GqaLayerW):
+            lw.q, lw.k, lw.v, lw.o = m4(w.q), m4(w.k), m4(w.v), m4(w.o)
+            lw.q_norm, lw.k_norm = arr(w.qn, np.uint16), arr(w.kn, np.uint16)
+        else:
+            lw.qkv, lw.z, lw.a, lw.b, lw.out = m4(w.qkv), m4(w.z), m4(w.a), m4(w.b), m4(w.out)
+            c = w.core
+            lw.conv_w, lw.dt_bias = arr(c.conv_w, np.uint16), arr(c.dt_bias, np.uint16)
+            lw.norm_w, lw.A_log = arr(c.norm_w, np.uint16), arr(c.A_log, np.float32)
+        _L.check(self.lib.ds4f_gpu_attn_weights(L, ctypes.byref(lw)), "ds4f_gpu_attn_weights")
+
+    def attn_step(self, L: int, token: int, state):
+        """One decode token of layer L on the residual stream; returns the
+        new state (ds4f_gpu_attn_step)."""
+        st = _f32(state).reshape(-1).copy()
+        _L.check(self.lib.ds4f_gpu_attn_step(L, token, _p(st)), "ds4f_gpu_attn_step")
+        return st
 
 
 def dptr(t) -> ctypes.c_void_p | None:

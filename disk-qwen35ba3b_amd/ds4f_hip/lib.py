@@ -26,6 +26,21 @@ class Geom(ctypes.Structure):
                  "lin_vd")]
 
 
+class Mlx4W(ctypes.Structure):
+    """Ds4fGpuMlx4W."""
+    _fields_ = [("vals", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("biases", ctypes.c_void_p), ("rows", ctypes.c_int), ("cols", ctypes.c_int)]
+
+
+class LayerW(ctypes.Structure):
+    """Ds4fGpuLayerW."""
+    _fields_ = ([("in_norm", ctypes.c_void_p)] +
+                [(n, Mlx4W) for n in ("q", "k", "v", "o")] +
+                [("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p)] +
+                [(n, Mlx4W) for n in ("qkv", "z", "a", "b", "out")] +
+                [(n, ctypes.c_void_p) for n in ("conv_w", "dt_bias", "norm_w", "A_log")])
+
+
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
@@ -52,6 +67,9 @@ _SIGS = {
     "ds4f_hip_synth_lin_state": ([_i, _d, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_conv_history": ([_i, _i, _u64, _u64, _vp], _i),
     "ds4f_gpu_last_error": ([], ctypes.c_char_p),
+    "ds4f_gpu_attn_weights": ([_i, ctypes.POINTER(LayerW)], _i),
+    "ds4f_gpu_attn_step": ([_i, _i, _vp], _i),
+    "ds4f_hip_attn_step_async": ([_i, _i, _vp, _vp], _i),
     "ds4f_gpu_mlx4_matvec": ([_vp, _vp, _vp, _i, _i, _vp, _vp], _i),
     "ds4f_gpu_mlx4_batch": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i], _i),
     "ds4f_hip_mlx4_matvec_async": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),

@@ -28,6 +28,7 @@ GQA_QGATE, GQA_K, GQA_V, GQA_QNW, GQA_KNW, GQA_KCACHE, GQA_VCACHE = 1, 2, 3, 4, 
 LIN_QKV, LIN_Z, LIN_A, LIN_B, LIN_CONVW, LIN_ALOG, LIN_DTB = 16, 17, 18, 19, 20, 21, 22
 LIN_NORMW, LIN_STATE, LIN_CONVSTATE = 23, 24, 25
 MLX4_Q, MLX4_SCALE, MLX4_BIAS, MLX4_X = 32, 33, 34, 35
+BLK_STATE, BLK_INNORM = 36, 37
 
 
 def tid(base: int, layer: int = 0, step: int = 0) -> int:

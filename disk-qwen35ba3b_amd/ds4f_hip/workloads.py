@@ -11,6 +11,9 @@ Shapes and distributions follow the five workloads the path is measured on:
 * GQA prefill and delta-rule prefill over T tokens (per-token tensors are
   the decode tensors at step = token index).
 * The 40-layer stack (GQA at layer % 4 == 3) decoding consecutive steps.
+* Whole attention layers (input RMSNorm, MLX 4-bit projections, the core,
+  the output projection and the residual) on a hidden state of 2048: the
+  projection weights are synthetic MLX 4-bit matrices (``mlx4_matrix``).
 
 All arrays are numpy; bf16 tensors are returned as uint16 bits (weights) or
 as float32 holding bf16 values (caches), matching what each side consumes.
@@ -156,14 +159,15 @@ def mlx4_pack(q: np.ndarray) -> np.ndarray:
     return (qq << (4 * np.arange(8, dtype=np.uint32))).sum(axis=1, dtype=np.uint64).astype(np.uint32)
 
 
-def mlx4_matrix(R: int, C: int, seed: int = 0, layer: int = 0, bias: bool = True):
+def mlx4_matrix(R: int, C: int, seed: int = 0, layer: int = 0, bias: bool = True,
+                scale=(0.002, 0.02)):
     """A synthetic MLX 4-bit affine [R x C] matrix: (vals U32, scales BF16,
     biases BF16 or None).  q uniform in 0..15; per 64-element group a scale
-    in U(0.002, 0.02) and a bias of -scale * U(6, 9), the shape an affine
+    in U(*scale) and a bias of -scale * U(6, 9), the shape an affine
     quantiser gives a zero-centred weight group (w = q * scale + bias)."""
     n, ng = R * C, (R * C + 63) // 64
     q = (S.draws(seed, S.tid(S.MLX4_Q, layer), 0, n) >> np.uint64(60)).astype(np.uint32)
-    sc = S.uniform(seed, S.tid(S.MLX4_SCALE, layer), ng, 0.002, 0.02)
+    sc = S.uniform(seed, S.tid(S.MLX4_SCALE, layer), ng, scale[0], scale[1])
     scales = S.bf16_bits(sc)
     biases = None
     if bias:
@@ -174,3 +178,80 @@ def mlx4_matrix(R: int, C: int, seed: int = 0, layer: int = 0, bias: bool = True
 def mlx4_x(C: int, seed: int = 0, layer: int = 0, step: int = 0) -> np.ndarray:
     """An input vector N(0, 1) of the matvec (fp32)."""
     return S.normal(seed, S.tid(S.MLX4_X, layer, step), C)
+
+
+@dataclass
+class Mlx4W:
+    """One MLX 4-bit weight: U32 nibble words, BF16 scales / biases per 64
+    elements, decoded shape rows x cols."""
+    vals: np.ndarray
+    scales: np.ndarray
+    biases: np.ndarray | None
+    rows: int
+    cols: int
+
+
+# Scales of the layers' projection weights: an affine 4-bit quantiser's
+# per-group step for weights of std about 0.02-0.03 (the scale of a 2048-wide
+# transformer's projections), so activations stay O(1) through the layer.
+PROJ_SCALE = (0.003, 0.010)
+
+
+def mlx4_weight(R: int, C: int, seed: int = 0, layer: int = 0, j: int = 0) -> Mlx4W:
+    """Projection j (0..7) of layer `layer`: its own streams."""
+    vals, scales, biases = mlx4_matrix(R, C, seed, 8 * layer + j, scale=PROJ_SCALE)
+    return Mlx4W(vals, scales, biases, R, C)
+
+
+def norm_weight(n: int, seed: int = 0, layer: int = 0) -> np.ndarray:
+    """input_layernorm weight bf16(1 + 0.1 N) [n] (uint16 bits)."""
+    return S.bf16_bits(S.normal(seed, S.tid(S.BLK_INNORM, layer), n, 1.0, 0.1))
+
+
+def hidden_state(hidden: int = 2048, seed: int = 0, step: int = 0) -> np.ndarray:
+    """A residual-stream vector N(0, 1) [hidden] (fp32)."""
+    return S.normal(seed, S.tid(S.BLK_STATE, 0, step), hidden)
+
+
+@dataclass
+class GqaLayerW:
+    """Weights of a full-GQA layer step (src/attn_qwen.c:87-225)."""
+    in_norm: np.ndarray   # uint16 [hidden]
+    q: Mlx4W              # [heads*2*d x hidden] (q | gate per head)
+    k: Mlx4W              # [kv_heads*d x hidden]
+    v: Mlx4W              # [kv_heads*d x hidden]
+    o: Mlx4W              # [hidden x heads*d]
+    qn: np.ndarray        # uint16 [d]
+    kn: np.ndarray        # uint16 [d]
+
+
+def gqa_layer_weights(g: GqaGeom, hidden: int = 2048, seed: int = 0, layer: int = 0) -> GqaLayerW:
+    qn, kn = gqa_weights(g, seed, layer)
+    return GqaLayerW(norm_weight(hidden, seed, layer),
+                     mlx4_weight(g.heads * 2 * g.head_dim, hidden, seed, layer, 0),
+                     mlx4_weight(g.kv_heads * g.head_dim, hidden, seed, layer, 1),
+                     mlx4_weight(g.kv_heads * g.head_dim, hidden, seed, layer, 2),
+                     mlx4_weight(hidden, g.heads * g.head_dim, seed, layer, 3), qn, kn)
+
+
+@dataclass
+class LinLayerW:
+    """Weights of a gated delta-rule layer step (src/attn_qwen.c:837-968)."""
+    in_norm: np.ndarray   # uint16 [hidden]
+    qkv: Mlx4W            # [rows x hidden]
+    z: Mlx4W              # [v_heads*vd x hidden]
+    a: Mlx4W              # [v_heads x hidden]
+    b: Mlx4W              # [v_heads x hidden]
+    out: Mlx4W            # [hidden x v_heads*vd]
+    core: LinWeights
+
+
+def lin_layer_weights(g: LinGeom, hidden: int = 2048, seed: int = 0, layer: int = 0) -> LinLayerW:
+    return LinLayerW(norm_weight(hidden, seed, layer),
+                     mlx4_weight(g.rows, hidden, seed, layer, 0),
+                     mlx4_weight(g.v_heads * g.vd, hidden, seed, layer, 1),
+                     mlx4_weight(g.v_heads, hidden, seed, layer, 2),
+                     mlx4_weight(g.v_heads, hidden, seed, layer, 3),
+                     mlx4_weight(hidden, g.v_heads * g.vd, seed, layer, 4),
+                     lin_weights(g, seed, layer))
+

@@ -209,6 +209,51 @@ int ds4f_hip_mlx4_matvec_async(const uint32_t *vals, const uint16_t *scales,
                                const uint16_t *biases, int R, int C,
                                const float *x, float *y, void *stream);
 
+/* ---- whole attention layers on the device (src/attn_qwen.c:87-225,
+ * :837-968) --------------------------------------------------------------- *
+ * One MLX 4-bit weight as the reference's mlx4_proj reads it from the trunk
+ * (src/attn_qwen.c:59-70): the U32 nibble tensor, its BF16 scales and
+ * optional BF16 biases, decoded shape rows x cols. */
+typedef struct Ds4fGpuMlx4W {
+    const uint32_t *vals;
+    const uint16_t *scales, *biases;
+    int rows, cols;
+} Ds4fGpuMlx4W;
+
+/* The weights of one attention layer (host pointers into the trunk; the
+ * roles of Ds4fTrunkLayout the reference's steps read).  A GQA layer fills
+ * in_norm, q, k, v, o, q_norm, k_norm (gqa_step :89-97); a linear layer
+ * in_norm, qkv, z, a, b, out, conv_w, A_log, dt_bias, norm_w (linear_step
+ * :840-849).  in_norm NULL means no input_layernorm (:158-159). */
+typedef struct Ds4fGpuLayerW {
+    const uint16_t *in_norm;
+    Ds4fGpuMlx4W q, k, v, o;
+    const uint16_t *q_norm, *k_norm;
+    Ds4fGpuMlx4W qkv, z, a, b, out;
+    const uint16_t *conv_w, *dt_bias, *norm_w;
+    const float *A_log;
+} Ds4fGpuLayerW;
+
+/* Upload layer L's weights to the device, keyed by the layer id (the trunk
+ * ring slot behind the pointers may be reused later, include/ds4f/ds4f.h:
+ * 172-174).  The layer must be bound (ds4f_gpu_attn_bind) with its kind;
+ * shapes are checked against the bound geometry and one hidden size for
+ * every layer (the projections' cols).  A second call replaces the copy. */
+int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w);
+
+/* One decode token of layer L on the residual stream, the whole of
+ * ds4f_attn_qwen_step for that layer (src/attn_qwen.c:1255-1264 ->
+ * gqa_step :87-225 or linear_step :837-968): xin = input_layernorm(state),
+ * the MLX 4-bit projections of xin, the attention core, the output
+ * projection, state += o.  state [hidden] is updated in place.  A layer of
+ * kind NONE and a token outside [0, max_tokens) are silent skips (0). */
+int ds4f_gpu_attn_step(int L, int token, float *state);
+/* The same with state in device memory, enqueued on `stream` (NULL: the
+ * plugin's stream); four launches (GQA: projections, split, merge, output)
+ * or three (linear: projections, core, output), no allocation, so a
+ * decode step can be captured in a HIP graph. */
+int ds4f_hip_attn_step_async(int L, int token, float *state, void *stream);
+
 /* Last error text of the plugin (static storage). */
 const char *ds4f_gpu_last_error(void);
 

@@ -58,8 +58,20 @@ def lib():
         L.orc_mlx4_decode.restype = None
         L.orc_mlx4_matvec.argtypes = [vp, vp, vp, i, i, vp, vp]
         L.orc_mlx4_matvec.restype = None
+        mp = ctypes.POINTER(_Mlx4)
+        L.orc_gqa_step.argtypes = [i, i, i, i, _f32p, i, i, _f32p, vp, mp, mp, mp, mp, _u16p, _u16p]
+        L.orc_gqa_step.restype = i
+        L.orc_lin_step.argtypes = [i, i, i, i, i, i, i, _f32p, _f32p, _f32p, vp, mp, mp, mp, mp, mp,
+                                   _u16p, _f32p, _u16p, _u16p]
+        L.orc_lin_step.restype = i
         _lib = L
     return _lib
+
+
+class _Mlx4(ctypes.Structure):
+    """OrcMlx4: one MLX 4-bit weight (q35_oracle.h)."""
+    _fields_ = [("vals", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("biases", ctypes.c_void_p), ("rows", ctypes.c_int), ("cols", ctypes.c_int)]
 
 
 def _c(a, dt):
@@ -167,3 +179,47 @@ def mlx4_matvec(vals, scales, biases, R, C, x):
     y = np.empty(R, np.float32)
     lib().orc_mlx4_matvec(_ptr(vals), _ptr(scales), _ptr(biases), R, C, _ptr(x), _ptr(y))
     return y
+
+
+def _mlx4(w, keep):
+    """OrcMlx4 of a weight with attributes vals, scales, biases, rows, cols;
+    the contiguous arrays are appended to `keep` to outlive the call."""
+    vals, scales = _c(w.vals, np.uint32), _c(w.scales, np.uint16)
+    biases = None if w.biases is None else _c(w.biases, np.uint16)
+    keep += [vals, scales, biases]
+    return ctypes.byref(_Mlx4(_ptr(vals), _ptr(scales), _ptr(biases), w.rows, w.cols))
+
+
+def gqa_step(kv_layer, token, state, w, heads, kv_heads, head_dim):
+    """One full-GQA layer step (orc_gqa_step) on the hidden state.  w has
+    in_norm, q, k, v, o, qn, kn (MLX 4-bit weights as in _mlx4).  kv_layer
+    is updated in place; returns the new state."""
+    st = _c(state, np.float32).copy()
+    keep = []
+    innorm = None if w.in_norm is None else _c(w.in_norm, np.uint16)
+    rc = lib().orc_gqa_step(heads, kv_heads, head_dim, kv_layer.shape[0], kv_layer, token,
+                            st.size, st, _ptr(innorm), _mlx4(w.q, keep), _mlx4(w.k, keep),
+                            _mlx4(w.v, keep), _mlx4(w.o, keep), _c(w.qn, np.uint16),
+                            _c(w.kn, np.uint16))
+    if rc != 0:
+        raise RuntimeError("orc_gqa_step failed")
+    return st
+
+
+def lin_step(conv_ring, S, token, state, w, k_heads, v_heads, kd, vd, max_tokens=1 << 30):
+    """One gated delta-rule layer step (orc_lin_step).  w has in_norm, qkv,
+    z, a, b, out and core (conv_w, A_log, dt_bias, norm_w).  conv_ring and S
+    are updated in place; returns the new state."""
+    st = _c(state, np.float32).copy()
+    keep = []
+    innorm = None if w.in_norm is None else _c(w.in_norm, np.uint16)
+    c = w.core
+    rc = lib().orc_lin_step(k_heads, v_heads, kd, vd, max_tokens, token, st.size, conv_ring, S,
+                            st, _ptr(innorm), _mlx4(w.qkv, keep), _mlx4(w.z, keep),
+                            _mlx4(w.a, keep), _mlx4(w.b, keep), _mlx4(w.out, keep),
+                            _c(c.conv_w, np.uint16), _c(c.A_log, np.float32),
+                            _c(c.dt_bias, np.uint16), _c(c.norm_w, np.uint16))
+    if rc != 0:
+        raise RuntimeError("orc_lin_step failed")
+    return st
+

@@ -316,3 +316,95 @@ void orc_mlx4_matvec(const uint32_t *vals, const uint16_t *scales,
         y[r] = acc;
     }
 }
+
+/* mlx4_proj (src/attn_qwen.c:59-70): y = W x, W rows x cols */
+static void mlx4_proj(const OrcMlx4 *w, const float *x, float *y) {
+    orc_mlx4_matvec(w->vals, w->scales, w->biases, w->rows, w->cols, x, y);
+}
+
+/* xin = input_layernorm(state), or a copy without a norm weight
+ * (src/attn_qwen.c:142-159, :913-930) */
+static void input_norm(const float *state, const uint16_t *in_norm, int hidden, float *xin) {
+    memcpy(xin, state, (size_t)hidden * sizeof(float));
+    if (in_norm) orc_rmsnorm(in_norm, hidden, xin);
+}
+
+int orc_gqa_step(int heads, int kv_heads, int kh, int max_tokens, float *kv_layer,
+                 int token, int hidden, float *state, const uint16_t *in_norm,
+                 const OrcMlx4 *wq, const OrcMlx4 *wk, const OrcMlx4 *wv,
+                 const OrcMlx4 *wo, const uint16_t *qn_w, const uint16_t *kn_w) {
+    if (wq->rows != heads * 2 * kh || wk->rows != kv_heads * kh || wv->rows != kv_heads * kh ||
+        wq->cols != hidden || wk->cols != hidden || wv->cols != hidden ||
+        wo->cols != heads * kh || wo->rows != hidden)
+        return -1;                                   /* :108-115 */
+    if (token < 0 || token >= max_tokens) return 0;  /* :117 */
+    float *xin = malloc((size_t)hidden * sizeof(float));
+    float *q = malloc((size_t)wq->rows * sizeof(float));
+    float *k = malloc((size_t)wk->rows * sizeof(float));
+    float *v = malloc((size_t)wv->rows * sizeof(float));
+    float *ao = malloc((size_t)heads * kh * sizeof(float));
+    float *o = malloc((size_t)hidden * sizeof(float));
+    int rc = -1;
+    if (xin && q && k && v && ao && o) {
+        input_norm(state, in_norm, hidden, xin);
+        mlx4_proj(wq, xin, q);                       /* :160-165 */
+        mlx4_proj(wk, xin, k);
+        mlx4_proj(wv, xin, v);
+        rc = orc_gqa_body(heads, kv_heads, kh, max_tokens, kv_layer, token, q, k, v, qn_w, kn_w, ao);
+        if (rc == 0) {
+            mlx4_proj(wo, ao, o);                    /* :196 */
+            for (int i = 0; i < hidden; i++) state[i] += o[i];   /* :222 */
+        }
+    }
+    free(xin);
+    free(q);
+    free(k);
+    free(v);
+    free(ao);
+    free(o);
+    return rc;
+}
+
+int orc_lin_step(int k_heads, int v_heads, int kd, int vd, int max_tokens, int token,
+                 int hidden, float *conv_ring, float *S, float *state,
+                 const uint16_t *in_norm, const OrcMlx4 *wqkv, const OrcMlx4 *wz,
+                 const OrcMlx4 *wa, const OrcMlx4 *wb, const OrcMlx4 *wout,
+                 const uint16_t *conv_w, const float *A_log, const uint16_t *dt_bias,
+                 const uint16_t *norm_w) {
+    const int qkv_rows = 2 * k_heads * kd + v_heads * vd;
+    if (wqkv->rows != qkv_rows || wz->rows != v_heads * vd || wout->rows != hidden ||
+        wa->rows != v_heads || wb->rows != v_heads || wqkv->cols != hidden ||
+        wz->cols != hidden || wa->cols != hidden || wb->cols != hidden ||
+        wout->cols != v_heads * vd)
+        return -1;                                   /* :870-879 */
+    if (token < 0 || token >= max_tokens) return 0;  /* :882 */
+    float *xin = malloc((size_t)hidden * sizeof(float));
+    float *qkv = malloc((size_t)qkv_rows * sizeof(float));
+    float *z = malloc((size_t)v_heads * vd * sizeof(float));
+    float *a = malloc((size_t)v_heads * sizeof(float));
+    float *b = malloc((size_t)v_heads * sizeof(float));
+    float *out = malloc((size_t)v_heads * vd * sizeof(float));
+    float *o = malloc((size_t)hidden * sizeof(float));
+    int rc = -1;
+    if (xin && qkv && z && a && b && out && o) {
+        input_norm(state, in_norm, hidden, xin);
+        mlx4_proj(wqkv, xin, qkv);                   /* :932-948 */
+        mlx4_proj(wz, xin, z);
+        mlx4_proj(wa, xin, a);                       /* :459-469 */
+        mlx4_proj(wb, xin, b);
+        rc = orc_lin_body(k_heads, v_heads, kd, vd, token, conv_ring, S, qkv, z, a, b, conv_w,
+                          A_log, dt_bias, norm_w, out);
+        if (rc == 0) {
+            mlx4_proj(wout, out, o);                 /* :771-776 */
+            for (int i = 0; i < hidden; i++) state[i] += o[i];   /* :832-833 */
+        }
+    }
+    free(xin);
+    free(qkv);
+    free(z);
+    free(a);
+    free(b);
+    free(out);
+    free(o);
+    return rc;
+}

@@ -10,7 +10,14 @@
  *   src/attn_qwen.c  ds4f_attn_gqa_chunk    :1222-1231 (serial prefill body loop)
  *   src/attn_qwen.c  ds4f_attn_linear_chunk :1088-1109 (serial prefill body loop)
  * with the projections (MLX-4bit matvecs) removed: the callers hand in the
- * post-projection activations, exactly what the reference's bodies receive.
+ * post-projection activations, exactly what the reference's bodies receive;
+ * and the whole layer steps around them,
+ *   src/attn_qwen.c  gqa_step          :87-225   (input norm, projections,
+ *                                                  body, o_proj, residual)
+ *   src/attn_qwen.c  linear_step       :837-968  (the same for a delta-rule
+ *                                                  layer, with lin_body's
+ *                                                  a / b and out projections)
+ * on the MLX 4-bit matvec of src/kernels.c :118-219.
  * It is compiled with gcc -std=c99 -O2 (no -mfma), which on x86-64 gives the
  * same unfused float evaluation the reference's ISO-C scalar build has.
  */
@@ -102,6 +109,37 @@ void orc_mlx4_decode(const uint32_t *vals, const uint16_t *scales,
  * ascending c. */
 void orc_mlx4_matvec(const uint32_t *vals, const uint16_t *scales,
                      const uint16_t *biases, int R, int C, const float *x, float *y);
+
+/* One MLX 4-bit weight as mlx4_proj hands it to ds4f_mlx4_matvec
+ * (src/attn_qwen.c:59-70): decoded shape rows x cols. */
+typedef struct OrcMlx4 {
+    const uint32_t *vals;
+    const uint16_t *scales, *biases;
+    int rows, cols;
+} OrcMlx4;
+
+/* Full-GQA layer step (gqa_step, src/attn_qwen.c:87-225) on the hidden
+ * state [hidden], in place: xin = input_layernorm(state) (:142-157; in_norm
+ * NULL: xin = state), q|gate, k, v = W xin (:160-165), the body (:172),
+ * o = W_o attn_out (:196), state += o (:222).  The residual adds to the raw
+ * state, the projections read the normed copy.  token outside
+ * [0, max_tokens) is the silent skip of :117 (state untouched). */
+int orc_gqa_step(int heads, int kv_heads, int kh, int max_tokens, float *kv_layer,
+                 int token, int hidden, float *state, const uint16_t *in_norm,
+                 const OrcMlx4 *wq, const OrcMlx4 *wk, const OrcMlx4 *wv,
+                 const OrcMlx4 *wo, const uint16_t *qn_w, const uint16_t *kn_w);
+
+/* Gated delta-rule layer step (linear_step, src/attn_qwen.c:837-968, with
+ * lin_body's a / b projections :459-469 and out_proj + residual :771-776,
+ * :832-833): xin = input_layernorm(state) (:913-928), qkv and z = W xin
+ * (:932-948), a and b = W xin, the body, state += W_out out.  token
+ * outside [0, max_tokens) is the silent skip of :882. */
+int orc_lin_step(int k_heads, int v_heads, int kd, int vd, int max_tokens, int token,
+                 int hidden, float *conv_ring, float *S, float *state,
+                 const uint16_t *in_norm, const OrcMlx4 *wqkv, const OrcMlx4 *wz,
+                 const OrcMlx4 *wa, const OrcMlx4 *wb, const OrcMlx4 *wout,
+                 const uint16_t *conv_w, const float *A_log, const uint16_t *dt_bias,
+                 const uint16_t *norm_w);
 
 #ifdef __cplusplus
 }

@@ -106,3 +106,44 @@ def lin_step(ring_hist, S, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, kh, vh,
     out = rmsnorm(o, bf(norm_w)) * (zz * sigmoid(zz))
     qkv_post = np.concatenate([q.reshape(-1), k.reshape(-1), v.reshape(-1)])
     return out.reshape(-1), Sn, qkv_post
+
+
+def mlx4_dense(w):
+    """Dense float64 [rows][cols] of an MLX 4-bit weight (attributes vals,
+    scales, biases, rows, cols), decoded from the format's definition:
+    element k = r*cols + c is nibble k % 8 (low first) of word k / 8, and
+    w = q * scale + bias with the BF16 scale / bias of group k / 64."""
+    n = w.rows * w.cols
+    k = np.arange(n, dtype=np.int64)
+    vals = np.asarray(w.vals, np.uint32)
+    q = ((vals[k >> 3] >> (4 * (k & 7)).astype(np.uint32)) & 0xF).astype(np.float64)
+    dense = q * bf(w.scales)[k // 64]
+    if w.biases is not None:
+        dense += bf(w.biases)[k // 64]
+    return dense.reshape(w.rows, w.cols)
+
+
+def gqa_block(kc, vc, state, w, token, heads, kv_heads, d):
+    """A full-GQA layer on the residual stream: state + o_proj(attn(
+    input_layernorm(state))).  Returns (new state, k_new normed + rotated)."""
+    xin = rmsnorm(state, bf(w.in_norm))
+    qg = (mlx4_dense(w.q) @ xin).reshape(heads, 2 * d)
+    k = (mlx4_dense(w.k) @ xin).reshape(kv_heads, d)
+    v = (mlx4_dense(w.v) @ xin).reshape(kv_heads, d)
+    out, kn = gqa_step(kc, vc, qg, k, v, w.qn, w.kn, token)
+    return np.asarray(state, np.float64) + mlx4_dense(w.o) @ out.reshape(-1), kn, v
+
+
+def lin_block(ring_hist, S, state, w, kh, vh, kd, vd):
+    """A gated delta-rule layer on the residual stream: state +
+    out_proj(core(input_layernorm(state))).  Returns (new state, S_new,
+    raw qkv of this token)."""
+    xin = rmsnorm(state, bf(w.in_norm))
+    qkv = mlx4_dense(w.qkv) @ xin
+    z = mlx4_dense(w.z) @ xin
+    a = mlx4_dense(w.a) @ xin
+    b = mlx4_dense(w.b) @ xin
+    c = w.core
+    out, Sn, _ = lin_step(ring_hist, S, qkv, z, a, b, c.conv_w, c.A_log, c.dt_bias, c.norm_w,
+                          kh, vh, kd, vd)
+    return np.asarray(state, np.float64) + mlx4_dense(w.out) @ out, Sn, qkv
