@@ -37,6 +37,12 @@ Other workloads (one JSON line each, same fields):
                 2048, 287 MB of nibbles, scales and biases: more than the
                 256 MB MALL, so the weight streams from HBM every call),
                 device-resident; HBM roofline.
+  block_decode  the same 40-layer stack at --ctx, whole attention layers on
+                the residual stream (input RMSNorm, MLX 4-bit q/k/v or
+                qkv/z/a/b projections, the core, the output projection and
+                the residual add: ds4f_hip_attn_step_async), 697 MB of
+                synthetic 4-bit weights; one HIP graph per step; HBM
+                roofline over the whole step's algorithmic bytes.
 """
 from __future__ import annotations
 
@@ -85,7 +91,8 @@ def main() -> int:
     ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill",
                                                                     "lin_prefill", "hbm_copy",
                                                                     "gqa_decode", "lin_decode",
-                                                                    "mlx4_head"])
+                                                                    "mlx4_head",
+                                                                    "block_decode"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     ap.add_argument("--npast", type=int, default=4096, help="cached positions (gqa_decode)")
     ap.add_argument("--rotate", type=int, default=0,
@@ -106,6 +113,8 @@ def main() -> int:
         return run_layer_decode(args)
     if args.workload == "mlx4_head":
         return run_mlx4_head(args)
+    if args.workload == "block_decode":
+        return run_block_decode(args)
     return run_stack_decode(args)
 
 
@@ -796,6 +805,164 @@ def run_mlx4_head(args) -> int:
     return 0
 
 
+
+def mlx4_bytes(R: int, C: int) -> int:
+    """HBM bytes of one MLX 4-bit weight: nibbles, BF16 scales and biases."""
+    return R * C // 2 + 2 * (R * C // 64) * 2
+
+
+def run_block_decode(args) -> int:
+    import numpy as np
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip import synth as S
+    from ds4f_hip import workloads as W
+    from ds4f_hip.attn import GpuAttention, KvCache, dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    gq, lg = W.GqaGeom(), W.LinGeom()
+    H = 2048
+    kinds = W.stack_kinds(40)
+    N, K, WU, seed = args.ctx, args.steps, args.warmup, args.seed
+    T = WU + K
+    max_tokens = N + T + 64
+    want_cpu = not args.no_cpu_baseline
+
+    cache = KvCache(40, max_tokens) if want_cpu else None
+    ga = GpuAttention(kinds, max_tokens, cache)
+    for Lr, kd in enumerate(kinds):
+        if kd == 2:
+            L.check(lib.ds4f_hip_synth_gqa_cache(Lr, N, seed, S.tid(S.GQA_KCACHE, Lr),
+                                                 S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
+        else:
+            L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr), None),
+                    "synth state")
+            L.check(lib.ds4f_hip_synth_conv_history(Lr, N, seed, S.tid(S.LIN_CONVSTATE, Lr),
+                                                    None), "synth conv")
+
+    # synthetic 4-bit weights: random nibbles, per-group scales in the
+    # projections' range and biases that centre each group, drawn on the
+    # device (torch generator seeded with --seed) and registered per layer
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    lo, hi = W.PROJ_SCALE
+
+    def m4(R, C):
+        n, ng = R * C, R * C // 64
+        vals = torch.randint(0, 256, (n // 2,), dtype=torch.uint8, device=dev, generator=gen)
+        sc = torch.rand(ng, device=dev, generator=gen) * (hi - lo) + lo
+        bi = -sc * (torch.rand(ng, device=dev, generator=gen) * 3.0 + 6.0)
+        u16 = lambda t: t.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+        return W.Mlx4W(vals.cpu().numpy().view(np.uint32), u16(sc), u16(bi), R, C)
+
+    weights, weight_bytes = {}, 0
+    for Lr, kd in enumerate(kinds):
+        in_norm = W.norm_weight(H, seed, Lr)
+        if kd == 2:
+            qn, kn = W.gqa_weights(gq, seed, Lr)
+            w = W.GqaLayerW(in_norm, m4(gq.heads * 2 * gq.head_dim, H),
+                            m4(gq.kv_heads * gq.head_dim, H), m4(gq.kv_heads * gq.head_dim, H),
+                            m4(H, gq.heads * gq.head_dim), qn, kn)
+            mats = (w.q, w.k, w.v, w.o)
+        else:
+            w = W.LinLayerW(in_norm, m4(lg.rows, H), m4(lg.v_heads * lg.vd, H), m4(lg.v_heads, H),
+                            m4(lg.v_heads, H), m4(H, lg.v_heads * lg.vd), W.lin_weights(lg, seed, Lr))
+            mats = (w.qkv, w.z, w.a, w.b, w.out)
+        ga.set_layer_weights(Lr, w)
+        weight_bytes += sum(mlx4_bytes(m.rows, m.cols) for m in mats)
+        if want_cpu:
+            weights[Lr] = w
+    states = torch.empty((T, H), dtype=torch.float32, device=dev)
+    for s in range(T):
+        L.check(lib.ds4f_hip_synth(dptr(states[s]), H, 0, 0, 0.0, 1.0, seed,
+                                   S.tid(S.BLK_STATE, 0, s), None), "synth state")
+    torch.cuda.synchronize()
+    if want_cpu:
+        ga.sync(-1, to_host=True, n_kv_tokens=N)
+        states0 = states.cpu().numpy()
+
+    def launch_step(s, stream):
+        for Lr in range(40):
+            L.check(lib.ds4f_hip_attn_step_async(Lr, N + s, dptr(states[s]), stream),
+                    f"layer {Lr} step {s}")
+
+    graphs = []
+    side = torch.cuda.Stream()
+    for s in range(T):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            launch_step(s, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for s in range(WU):
+        graphs[s].replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for s in range(WU, T):
+        graphs[s].replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    ev_sec = ev0.elapsed_time(ev1) * 1e-3
+    del graphs
+    if not bool(torch.isfinite(states).all()):
+        raise RuntimeError("block_decode: non-finite hidden state")
+    tok_s = K / sec
+    act_bytes = 10 * (4 * (16 * 512 + 2 * 512 + 4096) + 2 * 2 * H * 4) + \
+        30 * (4 * (8192 + 4096 + 64 + 4096) + 2 * 2 * H * 4)
+    step_bytes = [weight_bytes + 10 * gqa_layer_bytes(N + s) + 30 * LIN_LAYER_BYTES + act_bytes
+                  for s in range(WU, T)]
+    achieved = sum(step_bytes) / ev_sec / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "whole step: 40 x (mlx4 projections + core + mlx4 output/residual)",
+                "launches": K, "us_per_launch": round(ev_sec / K * 1e6, 2),
+                "bytes_per_launch": int(sum(step_bytes) / K)}
+
+    cpu = None
+    if want_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        O.lib()
+        done, spent = 0, 0.0
+        while done < 16 and (done == 0 or spent < args.cpu_seconds):
+            st = states0[done].copy()
+            c0 = time.perf_counter()
+            for Lr, kd in enumerate(kinds):
+                if kd == 2:
+                    st = O.gqa_step(cache.kv[Lr], N + done, st, weights[Lr], gq.heads,
+                                    gq.kv_heads, gq.head_dim)
+                else:
+                    st = O.lin_step(cache.conv[Lr], cache.lin[Lr], N + done, st, weights[Lr],
+                                    lg.k_heads, lg.v_heads, lg.kd, lg.vd)
+            spent += time.perf_counter() - c0
+            done += 1
+        cpu = {"value": round(done / spent, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{done} decode steps of the same 40 whole layers at {N} context, C "
+                         f"oracle gcc -O2 (layer steps incl. the 4-bit projections), 1 thread, "
+                         f"{spent:.1f} s"}
+
+    ga.close()
+    line = {"metric": "attention-block decode tokens/s (40 layers, projections included), "
+                      f"{N} ctx, 1 GPU",
+            "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+            "warmup": WU, "ms_per_step": round(sec / K * 1e3, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "mlx4-weights/bf16-kv/fp32",
+            "data": "synthetic (MLX 4-bit weights from a seeded torch generator, KV bf16 N(0,1), "
+                    "state N(0,0.05), hidden N(0,1))",
+            "config": {"workload": "qwen3.5-35b-a3b attention layers on the residual stream: "
+                                   "40 layers (30 gated delta-rule + 10 GQA), input norm, "
+                                   "4-bit projections, core, output projection, residual",
+                       "context": N, "layers": 40, "hidden": H, "weight_bytes": weight_bytes,
+                       "batch": 1, "graph_per_step": True},
+            "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
 if __name__ == "__main__":
     sys.exit(main())
-

@@ -8,8 +8,9 @@
  * of the flattened matrix is nibble k%8 of word k/8; a BF16 scale and bias
  * per 64 elements (group k/64, which may straddle rows); w = q*scale+bias.
  *
- * One wave per row, two rows in flight per iteration; lane l takes 32
- * consecutive elements (one 16-byte word load) of each 2048-column chunk.
+ * One wave per 8 / NCH rows (NCH = 2048-column chunks of x), their loads
+ * and the next rows' issued together; lane l takes 32 consecutive elements
+ * (one 16-byte word load) of each 2048-column chunk.
  * With C % 32 == 0 those 32 elements start 32-aligned in the flattened
  * index, so they lie in one group: the lane computes
  *     scale * sum_e q_e x_e + bias * sum_e x_e
@@ -69,8 +70,13 @@ __device__ __forceinline__ float nib_dot(u32x4_t w, const float (&x)[32]) {
     return a0 + a1;
 }
 
+/* rows a wave takes per iteration: 8 2048-column chunks' worth of loads */
 template <int NCH>
+constexpr int rows_per_wave() { return 8 / NCH; }
+
+template <int NCH, bool NORM>
 __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
+    constexpr int RP = rows_per_wave<NCH>();
     Mlx4Job j;
     if (p.jobs) {
         const Q35Mlx4Job &d = p.jobs[blockIdx.y];
@@ -80,28 +86,81 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
     }
     const int R = j.R, C = p.C, lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (NT / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (NT / 64);
-    if (2 * wave >= R) return;     /* a shorter job of a batch: no rows here */
+    if (RP * wave >= R) return;    /* a shorter job of a batch: no rows here */
+
+    bool live[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ch++) live[ch] = ch * CHUNK + 32 * lane < C;
+
+    /* range-checked views: rows at and past R read zero */
+    const size_t nel = (size_t)R * C;
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint32_t *>(j.vals)), 0, (int)(nel / 2), Q35_BUF_DW3);
+    const int ng = (int)((nel + 63) / 64);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(j.scales)), 0, 2 * ng, Q35_BUF_DW3);
+    const bool has_b = j.biases != nullptr;
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(has_b ? j.biases : j.scales)), 0, has_b ? 2 * ng : 0, Q35_BUF_DW3);
+
+    /* the nibble words, scales and biases of RP rows; rows at and past R
+     * (and dead lanes) point past the buffers and read zero, so every load
+     * is unconditional */
+    struct Rows {
+        u32x4_t w[RP][NCH];
+        uint32_t sc[RP][NCH], bi[RP][NCH];
+    };
+    auto load_rows = [&](int r0, Rows &q) {
+#pragma unroll
+        for (int u = 0; u < RP; u++)
+#pragma unroll
+            for (int ch = 0; ch < NCH; ch++) {
+                const int64_t k0 = (int64_t)(r0 + u) * C + ch * CHUNK + 32 * lane;
+                const bool in = live[ch] && r0 + u < R;
+                const int kk = in ? (int)(k0 >> 3) : (int)(nel / 8);
+                const int gg = in ? (int)(k0 >> 6) : ng;
+                q.w[u][ch] = __builtin_amdgcn_raw_buffer_load_b128(vr, 4 * kk, 0, 0);
+                q.sc[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2 * gg, 0, 0);
+                q.bi[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(br, 2 * gg, 0, 0);
+            }
+    };
+    /* the first rows' weights go out before x is read: the weight stream
+     * and the x / norm prologue share one memory round trip */
+    Rows cur;
+    load_rows(RP * wave, cur);
 
     /* x of this lane's columns and, with x_norm, its RMSNorm: the square
      * sum in double over the wave, r = sqrtf(mean + 1e-6), x / r * w with
-     * the reference's two roundings (src/attn_qwen.c:142-157) */
+     * the reference's two roundings (src/attn_qwen.c:142-157).  x and the
+     * norm weights are range-checked loads issued together (dead lanes read
+     * zero), so the prologue waits on one memory round trip with the first
+     * pair's weights. */
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<float *>(j.x)), 0, 4 * C, Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t nrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(NORM ? p.x_norm : reinterpret_cast<const uint16_t *>(j.x))),
+        0, NORM ? 2 * C : 0, Q35_BUF_DW3);
     float xv[NCH][32];
-    bool live[NCH];
+    u32x4_t nw[NCH][4];
 #pragma unroll
     for (int ch = 0; ch < NCH; ch++) {
         const int c0 = ch * CHUNK + 32 * lane;
-        live[ch] = c0 < C;
 #pragma unroll
         for (int q = 0; q < 8; q++) {
-            const float4 v = live[ch] ? *reinterpret_cast<const float4 *>(j.x + c0 + 4 * q)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
-            xv[ch][4 * q] = v.x;
-            xv[ch][4 * q + 1] = v.y;
-            xv[ch][4 * q + 2] = v.z;
-            xv[ch][4 * q + 3] = v.w;
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, 4 * (c0 + 4 * q), 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[ch][4 * q + e] = __uint_as_float(v[e]);
+        }
+        if (NORM) {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                nw[ch][q] = __builtin_amdgcn_raw_buffer_load_b128(nrs, 2 * (c0 + 8 * q), 0, 0);
         }
     }
-    if (p.x_norm) {
+    /* every prologue load is issued before the first wait: the scheduler
+     * would otherwise sink the weight loads below the norm's reduction */
+    __builtin_amdgcn_sched_barrier(0);
+    if (NORM) {
         double ss = 0.0;
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++)
@@ -110,20 +169,12 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
         ss = q35_wave_sum(ss);
         const float r = sqrtf((float)(ss / (double)C) + 1e-6f);
 #pragma unroll
-        for (int ch = 0; ch < NCH; ch++) {
-            const int c0 = ch * CHUNK + 32 * lane;
+        for (int ch = 0; ch < NCH; ch++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint4 wb = live[ch] ? *reinterpret_cast<const uint4 *>(p.x_norm + c0 + 8 * q)
-                                          : make_uint4(0, 0, 0, 0);
-                const uint32_t wv[4] = {wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float w = q35_bf2f((uint16_t)(wv[e >> 1] >> (16 * (e & 1))));
-                    xv[ch][8 * q + e] = xv[ch][8 * q + e] / r * w;
-                }
+            for (int e = 0; e < 32; e++) {
+                const float w = q35_bf2f((uint16_t)(nw[ch][e >> 3][(e >> 1) & 3] >> (16 * (e & 1))));
+                xv[ch][e] = xv[ch][e] / r * w;
             }
-        }
     }
 
     /* x scaled by the inverse fp8 nibble unit, and its plain sums, per chunk */
@@ -143,43 +194,47 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
         xs[ch] = s;
     }
 
-    /* range-checked views: rows at and past R read zero */
-    const size_t nel = (size_t)R * C;
-    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<uint32_t *>(j.vals)), 0, (int)(nel / 2), Q35_BUF_DW3);
-    const int ng = (int)((nel + 63) / 64);
-    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<uint16_t *>(j.scales)), 0, 2 * ng, Q35_BUF_DW3);
-    const bool has_b = j.biases != nullptr;
-    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<uint16_t *>(has_b ? j.biases : j.scales)), 0, has_b ? 2 * ng : 0, Q35_BUF_DW3);
-
-    for (int r0 = 2 * wave; r0 < R; r0 += 2 * nwaves) {
-        float part[2];
+    /* y of the rows for the residual add, lane u < RP holding row r0 + u (a
+     * view of length 0 reads zeros when the launch does not accumulate) */
+    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(j.y), 0, p.accumulate ? 4 * R : 0, Q35_BUF_DW3);
+    for (int r0 = RP * wave; r0 < R; r0 += RP * nwaves) {
+        /* the next rows and these rows' y are requested before these rows
+         * are consumed */
+        const float yv = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(yrs, lane < RP ? 4 * (r0 + lane) : 4 * R, 0, 0));
+        Rows nxt;
+        load_rows(r0 + RP * nwaves, nxt);
+        float part[RP];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int r = r0 + u;                      /* may be R: reads zero */
+        for (int u = 0; u < RP; u++) {
             float acc = 0.0f;
 #pragma unroll
             for (int ch = 0; ch < NCH; ch++) {
-                /* element index of this lane's first column; a dead lane
-                 * (column >= C) points past the buffer and reads zero */
-                const int64_t k0 = (int64_t)r * C + ch * CHUNK + 32 * lane;
-                const int kk = live[ch] ? (int)(k0 >> 3) : (int)(nel / 8);
-                const int gg = live[ch] ? (int)(k0 >> 6) : ng;
-                const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(vr, 4 * kk, 0, 0);
-                const float sc = q35_bf2f((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(sr, 2 * gg, 0, 0));
-                const float bi = q35_bf2f((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(br, 2 * gg, 0, 0));
-                acc = fmaf(sc, nib_dot(w, xr[ch]), fmaf(bi, xs[ch], acc));
+                const float sc = q35_bf2f((uint16_t)cur.sc[u][ch]);
+                const float bi = q35_bf2f((uint16_t)cur.bi[u][ch]);
+                acc = fmaf(sc, nib_dot(cur.w[u][ch], xr[ch]), fmaf(bi, xs[ch], acc));
             }
             part[u] = acc;
         }
+        /* row u's total lands in every lane; lane u stores it */
+        float t = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const float t = q35_wave_sum(part[u]);
-            if (lane == 0 && r0 + u < R) j.y[r0 + u] = p.accumulate ? j.y[r0 + u] + t : t;
+        for (int u = 0; u < RP; u++) {
+            const float tu = q35_wave_sum(part[u]);
+            t = lane == u ? tu : t;
         }
+        if (lane < RP && r0 + lane < R) j.y[r0 + lane] = p.accumulate ? yv + t : t;
+        cur = nxt;
     }
+}
+
+template <int NCH>
+void launch(const Q35Mlx4 *p, dim3 grid, hipStream_t stream) {
+    if (p->x_norm)
+        hipLaunchKernelGGL((mlx4_kernel<NCH, true>), grid, dim3(NT), 0, stream, *p);
+    else
+        hipLaunchKernelGGL((mlx4_kernel<NCH, false>), grid, dim3(NT), 0, stream, *p);
 }
 
 }  // namespace
@@ -192,17 +247,19 @@ extern "C" int q35_mlx4_supported(int R, int C) {
 extern "C" hipError_t q35_mlx4_matvec(const Q35Mlx4 *p, int njobs, hipStream_t stream) {
     if (!q35_mlx4_supported(p->R, p->C) || njobs < 1 || (njobs > 1 && !p->jobs))
         return hipErrorInvalidValue;
-    /* enough waves to keep the HBM pipes full, at least one row pair each */
-    int64_t pairs = ((int64_t)p->R + 1) / 2;
-    int64_t blocks = (pairs + NT / 64 - 1) / (NT / 64);
+    /* one wave per group of rows_per_wave rows, grid-strided beyond 2048
+     * workgroups */
+    const int nch = (p->C + CHUNK - 1) / CHUNK;
+    const int rp = nch == 1 ? rows_per_wave<1>() : nch == 2 ? rows_per_wave<2>() : rows_per_wave<4>();
+    const int64_t waves = ((int64_t)p->R + rp - 1) / rp;
+    int64_t blocks = (waves + NT / 64 - 1) / (NT / 64);
     if (blocks > 2048) blocks = 2048;
     const dim3 grid((unsigned)blocks, (unsigned)njobs);
-    const int nch = (p->C + CHUNK - 1) / CHUNK;
     if (nch == 1)
-        hipLaunchKernelGGL(mlx4_kernel<1>, grid, dim3(NT), 0, stream, *p);
+        launch<1>(p, grid, stream);
     else if (nch == 2)
-        hipLaunchKernelGGL(mlx4_kernel<2>, grid, dim3(NT), 0, stream, *p);
+        launch<2>(p, grid, stream);
     else
-        hipLaunchKernelGGL(mlx4_kernel<4>, grid, dim3(NT), 0, stream, *p);
+        launch<4>(p, grid, stream);
     return hipGetLastError();
 }
