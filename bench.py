@@ -611,12 +611,22 @@ def run_layer_decode(args) -> int:
 
 
 def lin_prefill_flops(T: int, C: int = 64, heads: int = 32, dk: int = 128, dv: int = 128) -> float:
-    """Algorithmic flops of the chunked delta-rule prefill, per (value head,
-    chunk): K K^T and Q K^T on their lower triangles, once per key head
-    (C^2 dk a value head); T = (I + A)^-1 (C^3 / 3); K S0, Q S0 and the
-    state update K^T Delta (6 C dk dv); T X and Pm Delta on their triangles
-    (2 C^2 dv).  Triangles are counted as C^2 / 2 entries, so the figure is
-    a lower bound on the work done."""
+    """Algorithmic flops of the chunked (WY) delta-rule prefill with every
+    intra-chunk product counted as a full matrix, per (value head, chunk):
+    2 C^2 (3 dk + 2 dv) for K K^T, Q K^T, the W / U products and their
+    applications, 6 C dk dv for K S0, Q S0 and K^T Delta, 2 C^3 / 3 for the
+    triangular inverse: 11,709,098.7 flop, 2.398e10 at 4096 tokens."""
+    per = 2.0 * C * C * (3 * dk + 2 * dv) + 6.0 * C * dk * dv + 2.0 * C ** 3 / 3.0
+    return per * heads * ((T + C - 1) // C)
+
+
+def lin_prefill_flops_useful(T: int, C: int = 64, heads: int = 32, dk: int = 128,
+                             dv: int = 128) -> float:
+    """The flops this build's T-form kernels issue as useful work, per (value
+    head, chunk): K K^T and Q K^T on their lower triangles, once per key head
+    (C^2 dk a value head); T = (I + A)^-1 (C^3 / 3); K S0, Q S0 and the state
+    update K^T Delta (6 C dk dv); T X and Pm Delta on their triangles
+    (2 C^2 dv): 16.29 GFLOP at 4096 tokens."""
     per = 1.0 * C * C * dk + C ** 3 / 3.0 + 6.0 * C * dk * dv + 2.0 * C * C * dv
     return per * heads * ((T + C - 1) // C)
 
@@ -684,7 +694,10 @@ def run_lin_prefill(args) -> int:
                 "traffic": load_traffic(f"lin_prefill_t{T}"),
                 "kernel": "delta prefill = conv + chunk + scan + gnorm kernels "
                           "(fp32 MFMA), state reset included",
-                "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops}
+                "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops,
+                "useful_flops_per_launch": lin_prefill_flops_useful(T),
+                "useful_frac": round(lin_prefill_flops_useful(T) / (op_us * 1e-6) / 1e12
+                                     / MFMA_F32_PEAK_TFLOPS, 4)}
 
     cpu = None
     if not args.no_cpu_baseline:

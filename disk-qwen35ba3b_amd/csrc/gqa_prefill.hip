@@ -13,10 +13,14 @@
  * 2. prefix: cache rows of positions before t0 (earlier chunks) into the
  *            fp16 key / value workspaces; zero padding rows (only launched
  *            when there are such rows).
- * 3. attn:   grid = (pairs of 16-position q blocks, kv heads), 4 waves.  A
- *            workgroup serves the 8 q heads of its kv head (wave w: heads
- *            2w, 2w+1 x 16 positions = 32 columns), so every K / V tile
- *            staged in LDS feeds 128 query rows.  Per 32-key block:
+ * 3. attn:   grid = (pairs of 16-position q blocks, kv heads), 8 waves in
+ *            two groups of 4.  A group serves the 8 q heads of its kv head
+ *            for one q block (wave w: heads 2w, 2w+1 x 16 positions = 32
+ *            columns); group A runs the long block's first key tiles,
+ *            group B the short block and then the long block's remaining
+ *            tiles, and hands its partial to group A through LDS at the
+ *            end, so every workgroup (and each SIMD's two waves) carries
+ *            the same causal work.  Per 32-key block:
  *              S^T[32 key][32 q] = K Q^T   (16 x v_mfma_f32_32x32x16_f16),
  *              online softmax per column (rescaled only when a column max
  *              grows by more than 8 in scaled units, which keeps P <= e^8
@@ -24,10 +28,11 @@
  *              O^T[256][32 q] += V^T P^T  (16 x 32x32x16 f16; the S^T
  *              accumulator registers are P's B operand as they stand, the
  *              value tile is stored in the matching key order).
- *            Output O / l times sigmoid(gate), fp32.  K / V tiles move
- *            global -> registers (buffer loads, one tile ahead) -> padded
- *            LDS (two stages); each workgroup runs a long and a short q
- *            block so every workgroup carries the same causal work.
+ *            Output O / l times sigmoid(gate), fp32.  K / V tiles go
+ *            global -> LDS by direct-to-LDS buffer loads into two stages
+ *            per group; the K workspace is granule-major and the V
+ *            workspace row-swizzled, so each stage is a verbatim copy and
+ *            the operand reads are bank-conflict free.
  * Operands are fp16 (11-bit mantissa): a single MFMA pass keeps the
  * outputs within the parity bar (max abs error ~1e-3 against the fp32
  * reference at T = 4096), where bf16 operands would not.

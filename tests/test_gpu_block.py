@@ -124,3 +124,48 @@ def test_step_silent_skips():
         assert np.array_equal(ga.attn_step(0, -1, st), st)
     finally:
         ga.close()
+
+
+def test_step_graph_replays_match_oracle():
+    """Layer steps of three tokens captured as HIP graphs (the way a decode
+    loop runs them) and replayed in order with eager work between replays;
+    every replay's hidden state matches the oracle."""
+    import ctypes
+
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip.attn import dptr
+
+    kinds = [1, 2]
+    n_past = 50
+    ga, ref, ws = _stack(kinds, n_past, n_past, 256)
+    try:
+        dev = torch.device("cuda:0")
+        states = [W.hidden_state(HID, 0, 300 + s) for s in range(3)]
+        d_states = torch.tensor(np.stack(states), device=dev)
+        side = torch.cuda.Stream()
+        graphs = []
+        for s in range(3):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                for Lr in range(len(kinds)):
+                    L.check(ga.lib.ds4f_hip_attn_step_async(Lr, n_past + s, dptr(d_states[s]), st),
+                            "attn step capture")
+            graphs.append(g)
+        torch.cuda.synchronize()
+        for s in range(3):
+            graphs[s].replay()
+            torch.cuda.synchronize()
+            scratch = torch.randn(1 << 20, device=dev)          # eager work between replays
+            float((scratch * 2.0).sum().item())
+            got = d_states[s].cpu().numpy()
+            st_o = states[s]
+            for Lr, k in enumerate(kinds):
+                st_o = _oracle_layer(k, ref[Lr], ws[Lr], n_past + s, st_o)
+            mx, rr = _err(got, st_o)
+            _say(f"graph replay token {n_past + s}: max|err| {mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+    finally:
+        ga.close()
