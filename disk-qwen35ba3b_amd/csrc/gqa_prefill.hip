@@ -423,19 +423,24 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
         for (int i = 1; i < 16; i++) mx = fmaxf(mx, s[i]);
         mx = half_pair_max(mx);
         const bool need = mx > m_used + RESCALE_MARGIN / SCALE;
+        /* A column whose keys so far were all masked keeps m_used = -inf
+         * and weights 0 (group B's first tile of the long block can lie
+         * wholly after the block's first positions when t0 is not a multiple
+         * of 16): its factor is 1, not exp2(-inf - -inf), and its exponent
+         * offset stays finite.  need implies a finite mx, so a first use
+         * gives exp2(-inf) = 0. */
         if (__any(need)) {
-            const float m_new = need ? mx : m_used;
-            const float alpha = exp2f_fast((m_used - m_new) * EXP_K);   /* -inf -> 0 on first use */
+            const float alpha = need ? exp2f_fast((m_used - mx) * EXP_K) : 1.0f;
             l_run *= alpha;
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 acc[dt] *= alpha;
                 __builtin_amdgcn_sched_barrier(0);
             }
-            m_used = m_new;
+            m_used = need ? mx : m_used;
         }
         f16x8_t pb[2];
-        const float mk = m_used * EXP_K;
+        const float mk = m_used == -INFINITY ? 0.0f : m_used * EXP_K;
 #pragma unroll
         for (int i = 0; i < 16; i++) pb[i >> 3][i & 7] = (_Float16)exp2f_fast(fmaf(s[i], EXP_K, -mk));
         /* the row sum of the fp16 weights the PV product uses, two a step */

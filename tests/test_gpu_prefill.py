@@ -120,6 +120,39 @@ def test_gqa_prefill_continues_a_cache():
     ga.close()
 
 
+@pytest.mark.parametrize("t0,B", [(37, 100), (45, 200), (13, 33), (3, 250)])
+def test_gqa_prefill_unaligned_start(t0, B):
+    """Prefill at t0 not a multiple of 16 over a cache of t0 past rows.
+    These (t0, B) give the workgroup that pairs q blocks so that its second
+    wave group starts the long block at a key tile lying wholly after the
+    first positions of that block (tile 4 of t0 = 37, B = 100 starts at key
+    128 for q positions 117..132): those columns see no valid key in the
+    tile and must contribute nothing, not a NaN."""
+    qn, kn = W.gqa_weights(GQ)
+    q, k, v = W.gqa_prefill_tokens(GQ, t0 + B)
+    cache = KvCache(1, t0 + B + 16)
+    ref_kv = cache.kv[0].copy()
+    ga = GpuAttention([2], t0 + B + 16, cache)
+    try:
+        past = slice(0, t0)
+        ga.gqa_prefill(0, 0, q[past].reshape(t0, -1), k[past].reshape(t0, -1),
+                       v[past].reshape(t0, -1), qn, kn)
+        O.gqa_prefill(ref_kv, 0, q[past].reshape(t0, -1), k[past].reshape(t0, -1),
+                      v[past].reshape(t0, -1), qn, kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+        ref_kv[past] = S.bf16_round(ref_kv[past])
+        sl = slice(t0, t0 + B)
+        out, _ = ga.gqa_prefill(0, t0, q[sl].reshape(B, -1), k[sl].reshape(B, -1),
+                                v[sl].reshape(B, -1), qn, kn)
+        ref, _ = O.gqa_prefill(ref_kv, t0, q[sl].reshape(B, -1), k[sl].reshape(B, -1),
+                               v[sl].reshape(B, -1), qn, kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+        mx, rr = _err(out, ref)
+        _say(f"gqa prefill t0={t0} B={B}: max abs {mx:.3e} rel-rms {rr:.3e}")
+        assert np.isfinite(out).all()
+        assert mx <= ATOL
+    finally:
+        ga.close()
+
+
 # ------------------------------------------------------------------ delta rule
 LG = W.LinGeom()
 STATE_RTOL = 1e-4
