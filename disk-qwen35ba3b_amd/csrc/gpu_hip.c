@@ -56,6 +56,11 @@ static struct Plugin {
     int hidden;
     struct LayerW *lw;         /* [n_layers] */
     float *d_act, *d_state;
+    /* whole-layer chunks: X operands and projection outputs */
+    void *d_chunk;
+    int chunk_cap;             /* token rows (a multiple of the GEMM's M tile) */
+    float *h_states;           /* pinned staging of the host chunk entry */
+    size_t h_states_cap;
 } P;
 
 static void set_err(const char *fmt, ...) {
@@ -880,6 +885,8 @@ typedef struct LayerW {
     Q35Mlx4 out;               /* output projection: x, y set per call */
     const uint16_t *qn, *kn, *conv_w, *dt_bias, *norm_w;
     const float *A_log;
+    Q35Mlx4GemmJob *gjobs;     /* device: the chunk GEMMs' projections, then the output */
+    int gmax;                  /* widest projection */
 } LayerW;
 
 /* activations between the launches of one layer step, floats */
@@ -911,8 +918,14 @@ static void layers_free(void) {
     }
     if (P.d_act) hipFree(P.d_act);
     if (P.d_state) hipFree(P.d_state);
+    if (P.d_chunk) hipFree(P.d_chunk);
+    if (P.h_states) hipHostFree(P.h_states);
     P.lw = NULL;
     P.d_act = P.d_state = NULL;
+    P.d_chunk = NULL;
+    P.h_states = NULL;
+    P.chunk_cap = 0;
+    P.h_states_cap = 0;
     P.hidden = 0;
 }
 
@@ -1017,13 +1030,20 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
         np = 4;
         outw = &w->out;
     }
-    Part pt[32];
-    const void *pv[5], *ps[5], *pb[5], *in_norm, *jobs, *t0, *t1, *t2, *t3;
+    Part pt[40];
+    const void *pv[5], *ps[5], *pb[5], *psb[5], *in_norm, *jobs, *gjobs, *t0, *t1, *t2, *t3;
     int n = 0;
     for (int i = 0; i < np; i++) n += mlx4_parts(pt + n, proj[i], &pv[i], &ps[i], &pb[i]);
     n += mlx4_parts(pt + n, outw, &pv[4], &ps[4], &pb[4]);
+    /* (s, b - 1024 s) per row and 64-column group of each weight, for the
+     * chunk GEMMs (filled on the device below) */
+    for (int i = 0; i < 5; i++) {
+        const Ds4fGpuMlx4W *m = i < 4 ? (i < np ? proj[i] : NULL) : outw;
+        pt[n++] = (Part){NULL, m ? (size_t)m->rows * (m->cols / 64) * sizeof(Q35Mlx4SB) : 0, &psb[i]};
+    }
     pt[n++] = (Part){w->in_norm, w->in_norm ? (size_t)hidden * 2 : 0, &in_norm};
     pt[n++] = (Part){NULL, (size_t)np * sizeof(Q35Mlx4Job), &jobs};   /* filled below */
+    pt[n++] = (Part){NULL, (size_t)(np + 1) * sizeof(Q35Mlx4GemmJob), &gjobs};
     if (kind == DS4F_LAYER_GQA) {
         pt[n++] = (Part){w->q_norm, GQA_D * 2, &t0};
         pt[n++] = (Part){w->k_norm, GQA_D * 2, &t1};
@@ -1055,6 +1075,32 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
     }
     lw->jobs = (Q35Mlx4Job *)jobs;
     lw->njobs = np;
+    /* the chunk GEMMs' job table: the np projections, then the output */
+    Q35Mlx4GemmJob gj[5];
+    int ng = 0;
+    lw->gmax = 0;
+    for (int i = 0; i < 5; i++) {
+        const Ds4fGpuMlx4W *m = i < 4 ? (i < np ? proj[i] : NULL) : outw;
+        if (!m) continue;
+        if (q35_mlx4_sb((const uint16_t *)ps[i], (const uint16_t *)pb[i], (Q35Mlx4SB *)psb[i],
+                        (int64_t)m->rows * (m->cols / 64), P.stream) != hipSuccess ||
+            hipStreamSynchronize(P.stream) != hipSuccess) {
+            set_err("layer weights: scale table failed");
+            hipFree(lw->d);
+            memset(lw, 0, sizeof *lw);
+            return -1;
+        }
+        gj[ng++] = (Q35Mlx4GemmJob){(const uint32_t *)pv[i], (const Q35Mlx4SB *)psb[i], m->rows};
+        if (i < 4 && m->rows > lw->gmax) lw->gmax = m->rows;
+    }
+    if (hipMemcpy((void *)gjobs, gj, (size_t)ng * sizeof(Q35Mlx4GemmJob), hipMemcpyHostToDevice) !=
+        hipSuccess) {
+        set_err("layer weights: GEMM job table upload failed");
+        hipFree(lw->d);
+        memset(lw, 0, sizeof *lw);
+        return -1;
+    }
+    lw->gjobs = (Q35Mlx4GemmJob *)gjobs;
     lw->in_norm = (const uint16_t *)in_norm;
     memset(&lw->out, 0, sizeof lw->out);
     lw->out.vals = (const uint32_t *)pv[4];
@@ -1140,3 +1186,186 @@ int ds4f_gpu_attn_step(int L, int token, float *state) {
     return 0;
 }
 
+
+/* ---- whole-layer chunks (ds4f_attn_gqa_chunk :1145-1252,
+ * ds4f_attn_linear_chunk :977-1135) ------------------------------------- */
+
+/* chunk workspace of mpad token rows: X operands (hi, lo, group sums) for
+ * K up to 4096, the projection outputs of either layer kind, the core's
+ * output; grow-only */
+enum { CH_Q, CH_K, CH_V, CH_AO, CH_QKV, CH_Z, CH_A, CH_B, CH_LO, CH_N };
+
+static size_t ch_width(int i) {
+    switch (i) {
+    case CH_Q: return (size_t)P.g.n_heads * 2 * GQA_D;
+    case CH_K: case CH_V: return (size_t)P.g.n_kv_heads * GQA_D;
+    case CH_AO: return (size_t)P.g.n_heads * GQA_D;
+    case CH_QKV: return (size_t)P.rows;
+    case CH_Z: case CH_LO: return (size_t)P.vh * P.vd;
+    default: return (size_t)P.vh;
+    }
+}
+
+static size_t ch_kmax(void) {
+    size_t k = (size_t)P.hidden;
+    if (ch_width(CH_AO) > k) k = ch_width(CH_AO);
+    if (ch_width(CH_LO) > k) k = ch_width(CH_LO);
+    return k;
+}
+
+typedef struct { uint16_t *xh, *xl; float *xsum; float *out[CH_N]; } ChunkWs;
+
+/* byte offsets of the workspace parts for mpad rows; the total when ws is
+ * NULL, else ws filled with pointers into P.d_chunk */
+static size_t chunk_layout(int mpad, ChunkWs *ws) {
+    const size_t K = ch_kmax();
+    size_t sizes[3 + CH_N], off[3 + CH_N], total = 0;
+    sizes[0] = sizes[1] = (size_t)mpad * K * 2;
+    sizes[2] = (K / 64) * (size_t)mpad * 4;
+    for (int i = 0; i < CH_N; i++) sizes[3 + i] = (size_t)mpad * ch_width(i) * 4;
+    for (int i = 0; i < 3 + CH_N; i++) {
+        off[i] = total;
+        total += (sizes[i] + 255) & ~(size_t)255;
+    }
+    if (ws) {
+        char *b = (char *)P.d_chunk;
+        ws->xh = (uint16_t *)(b + off[0]);
+        ws->xl = (uint16_t *)(b + off[1]);
+        ws->xsum = (float *)(b + off[2]);
+        for (int i = 0; i < CH_N; i++) ws->out[i] = (float *)(b + off[3 + i]);
+    }
+    return total;
+}
+
+static int ensure_chunk(int B, ChunkWs *ws) {
+    const int mt = q35_mlx4_gemm_mtile();
+    const int mpad = (B + mt - 1) / mt * mt;
+    if (mpad > P.chunk_cap) {
+        if (P.d_chunk) {
+            HIPCHK(hipStreamSynchronize(P.stream));
+            hipFree(P.d_chunk);
+        }
+        P.d_chunk = NULL;
+        P.chunk_cap = 0;
+        HIPCHK(hipMalloc(&P.d_chunk, chunk_layout(mpad, NULL)));
+        P.chunk_cap = mpad;
+    }
+    chunk_layout(P.chunk_cap, ws);
+    return 0;
+}
+
+/* X = [norm](x rows), then y = X W^T for the njobs GEMM jobs of a device
+ * job table, job j writing ys[j] [B][lds[j]] */
+static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, int B,
+                      const Q35Mlx4GemmJob *jobs, int njobs, int max_n, float *const *ys,
+                      const int *lds, int accumulate, const ChunkWs *ws, hipStream_t st) {
+    Q35Mlx4Xprep xp = {x, norm_w, ws->xh, ws->xl, ws->xsum, B, P.chunk_cap, K, ldx};
+    HIPCHK(q35_mlx4_xprep(&xp, st));
+    Q35Mlx4Gemm g;
+    memset(&g, 0, sizeof g);
+    g.xh = ws->xh;
+    g.xl = ws->xl;
+    g.xsum = ws->xsum;
+    g.jobs = jobs;
+    for (int j = 0; j < njobs; j++) {
+        g.y[j] = ys[j];
+        g.ldy[j] = lds[j];
+    }
+    g.M = B;
+    g.Mpad = P.chunk_cap;
+    g.K = K;
+    g.accumulate = accumulate;
+    HIPCHK(q35_mlx4_gemm(&g, njobs, max_n, st));
+    return 0;
+}
+
+int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers) return -1;
+    const int kind = P.kind[L];
+    if (kind == DS4F_LAYER_NONE || B < 1) return 0;
+    if (!P.lw || !P.lw[L].d) {
+        set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
+        return -1;
+    }
+    if (t0 < 0 || t0 >= P.g.max_tokens) return 0;           /* :117, :882 */
+    if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
+    if (P.hidden % 64 != 0 || ch_kmax() % 64 != 0) {
+        set_err("chunk GEMM needs widths that are multiples of 64");
+        return -1;
+    }
+    const LayerW *lw = &P.lw[L];
+    hipStream_t st = pick(stream);
+    ChunkWs ws;
+    if (ensure_chunk(B, &ws) != 0) return -1;
+    const int H = P.hidden;
+    /* the projections of the B normed rows */
+    const int outs[4] = {kind == DS4F_LAYER_GQA ? CH_Q : CH_QKV, kind == DS4F_LAYER_GQA ? CH_K : CH_Z,
+                         kind == DS4F_LAYER_GQA ? CH_V : CH_A, CH_B};
+    float *ys[4];
+    int lds[4];
+    for (int j = 0; j < lw->njobs; j++) {
+        ys[j] = ws.out[outs[j]];
+        lds[j] = (int)ch_width(outs[j]);
+    }
+    if (chunk_gemm(states, H, lw->in_norm, H, B, lw->gjobs, lw->njobs, lw->gmax, ys, lds, 0, &ws,
+                   st) != 0)
+        return -1;
+    /* the core over the chunk */
+    int core_out;
+    if (kind == DS4F_LAYER_GQA) {
+        if (ds4f_hip_gqa_prefill_async(L, t0, B, ws.out[CH_Q], ws.out[CH_K], ws.out[CH_V], lw->qn,
+                                       lw->kn, ws.out[CH_AO], NULL, st) != 0)
+            return -1;
+        core_out = CH_AO;
+    } else {
+        if (ds4f_hip_lin_prefill_async(L, t0, B, ws.out[CH_QKV], ws.out[CH_Z], ws.out[CH_A],
+                                       ws.out[CH_B], lw->conv_w, lw->A_log, lw->dt_bias,
+                                       lw->norm_w, ws.out[CH_LO], NULL, st) != 0)
+            return -1;
+        core_out = CH_LO;
+    }
+    /* the output projection, added to the rows' states */
+    float *yo[1] = {states};
+    const int ldo[1] = {H};
+    return chunk_gemm(ws.out[core_out], (int)ch_width(core_out), NULL, (int)ch_width(core_out), B,
+                      lw->gjobs + lw->njobs, 1, H, yo, ldo, 1, &ws, st);
+}
+
+int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers) return -1;
+    if (P.kind[L] == DS4F_LAYER_NONE || B < 1 || t0 < 0 || t0 >= P.g.max_tokens) return 0;
+    if (!P.lw || !P.lw[L].d) {
+        set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
+        return -1;
+    }
+    if (forced_failure()) return fail_over(t0);
+    if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
+    const size_t row = (size_t)P.hidden * sizeof(float), bytes = (size_t)B * row;
+    if (bytes > P.h_states_cap) {
+        if (P.h_states) hipHostFree(P.h_states);
+        P.h_states = NULL;
+        P.h_states_cap = 0;
+        if (hipHostMalloc((void **)&P.h_states, bytes, hipHostMallocDefault) != hipSuccess) {
+            set_err("chunk: pinned staging failed");
+            return fail_over(t0);
+        }
+        P.h_states_cap = bytes;
+    }
+    if (ensure_stage(bytes, 0) != 0) return fail_over(t0);
+    for (int b = 0; b < B; b++) memcpy((char *)P.h_states + b * row, states[b], row);
+    if (hipMemcpyAsync(P.d_stage, P.h_states, bytes, hipMemcpyHostToDevice, P.stream) != hipSuccess ||
+        ds4f_hip_attn_chunk_async(L, t0, B, (float *)P.d_stage, NULL) != 0 ||
+        hipMemcpyAsync(P.h_states, P.d_stage, bytes, hipMemcpyDeviceToHost, P.stream) != hipSuccess ||
+        hipStreamSynchronize(P.stream) != hipSuccess)
+        return fail_over(t0);
+    for (int b = 0; b < B; b++) memcpy(states[b], (char *)P.h_states + b * row, row);
+    return 0;
+}

@@ -152,6 +152,16 @@ class GpuAttention:
         return st
 
 
+    def attn_chunk(self, L: int, t0: int, states):
+        """A prefill chunk of the tokens t0.. of layer L on their hidden
+        states [B][hidden]; returns the new states (ds4f_gpu_attn_chunk)."""
+        st = np.array(states, dtype=np.float32, order="C", copy=True)
+        B = st.shape[0]
+        ptrs = (ctypes.c_void_p * B)(*[st[b].ctypes.data for b in range(B)])
+        _L.check(self.lib.ds4f_gpu_attn_chunk(L, t0, B, ptrs), "ds4f_gpu_attn_chunk")
+        return st
+
+
 def dptr(t) -> ctypes.c_void_p | None:
     """Device pointer of a torch tensor (None passes NULL)."""
     return None if t is None else ctypes.c_void_p(t.data_ptr())

@@ -70,6 +70,8 @@ _SIGS = {
     "ds4f_gpu_attn_weights": ([_i, ctypes.POINTER(LayerW)], _i),
     "ds4f_gpu_attn_step": ([_i, _i, _vp], _i),
     "ds4f_hip_attn_step_async": ([_i, _i, _vp, _vp], _i),
+    "ds4f_gpu_attn_chunk": ([_i, _i, _i, ctypes.POINTER(ctypes.c_void_p)], _i),
+    "ds4f_hip_attn_chunk_async": ([_i, _i, _i, _vp, _vp], _i),
     "ds4f_gpu_mlx4_matvec": ([_vp, _vp, _vp, _i, _i, _vp, _vp], _i),
     "ds4f_gpu_mlx4_batch": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i], _i),
     "ds4f_hip_mlx4_matvec_async": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),

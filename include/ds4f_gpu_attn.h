@@ -254,6 +254,22 @@ int ds4f_gpu_attn_step(int L, int token, float *state);
  * decode step can be captured in a HIP graph. */
 int ds4f_hip_attn_step_async(int L, int token, float *state, void *stream);
 
+/* A prefill chunk of B tokens t0 .. t0+B-1 of layer L on the residual
+ * stream: the whole of ds4f_attn_gqa_chunk (src/attn_qwen.c:1145-1252) or
+ * ds4f_attn_linear_chunk (:977-1135), as src/main.c:604-660 calls them per
+ * layer: the tokens' input_layernorm, the batched MLX 4-bit projections
+ * (ds4f_mlx4_matvec_batch, src/kernels.c:581-619, here one fp16-MFMA GEMM
+ * launch for all of a layer's projections), the layer's prefill core, the
+ * batched output projection and the residual adds.  states holds B
+ * pointers to the tokens' hidden states [hidden], updated in place.  The
+ * results are those of B ds4f_gpu_attn_step calls in token order, up to
+ * float32 summation order. */
+int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states);
+/* The same with the states in device memory, [B][hidden] contiguous,
+ * enqueued on `stream`.  Allocates its workspace on first use or growth
+ * (not capturable then). */
+int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream);
+
 /* Last error text of the plugin (static storage). */
 const char *ds4f_gpu_last_error(void);
 

@@ -64,6 +64,12 @@ def lib():
         L.orc_lin_step.argtypes = [i, i, i, i, i, i, i, _f32p, _f32p, _f32p, vp, mp, mp, mp, mp, mp,
                                    _u16p, _f32p, _u16p, _u16p]
         L.orc_lin_step.restype = i
+        L.orc_gqa_chunk.argtypes = [i, i, i, i, _f32p, i, i, i, _f32p, vp, mp, mp, mp, mp, _u16p,
+                                    _u16p]
+        L.orc_gqa_chunk.restype = i
+        L.orc_lin_chunk.argtypes = [i, i, i, i, i, i, i, i, _f32p, _f32p, _f32p, vp, mp, mp, mp,
+                                    mp, mp, _u16p, _f32p, _u16p, _u16p]
+        L.orc_lin_chunk.restype = i
         _lib = L
     return _lib
 
@@ -221,5 +227,37 @@ def lin_step(conv_ring, S, token, state, w, k_heads, v_heads, kd, vd, max_tokens
                             _c(c.dt_bias, np.uint16), _c(c.norm_w, np.uint16))
     if rc != 0:
         raise RuntimeError("orc_lin_step failed")
+    return st
+
+
+def gqa_chunk(kv_layer, t0, states, w, heads, kv_heads, head_dim):
+    """A GQA prefill chunk on states [B][hidden] (orc_gqa_chunk); kv_layer
+    is updated in place; returns the new states."""
+    st = np.array(states, dtype=np.float32, order="C", copy=True)
+    keep = []
+    innorm = None if w.in_norm is None else _c(w.in_norm, np.uint16)
+    rc = lib().orc_gqa_chunk(heads, kv_heads, head_dim, kv_layer.shape[0], kv_layer, t0,
+                             st.shape[0], st.shape[1], st, _ptr(innorm), _mlx4(w.q, keep),
+                             _mlx4(w.k, keep), _mlx4(w.v, keep), _mlx4(w.o, keep),
+                             _c(w.qn, np.uint16), _c(w.kn, np.uint16))
+    if rc != 0:
+        raise RuntimeError("orc_gqa_chunk failed")
+    return st
+
+
+def lin_chunk(conv_ring, S, t0, states, w, k_heads, v_heads, kd, vd, max_tokens=1 << 30):
+    """A delta-rule prefill chunk on states [B][hidden] (orc_lin_chunk);
+    conv_ring and S are updated in place; returns the new states."""
+    st = np.array(states, dtype=np.float32, order="C", copy=True)
+    keep = []
+    innorm = None if w.in_norm is None else _c(w.in_norm, np.uint16)
+    c = w.core
+    rc = lib().orc_lin_chunk(k_heads, v_heads, kd, vd, max_tokens, t0, st.shape[0], st.shape[1],
+                             conv_ring, S, st, _ptr(innorm), _mlx4(w.qkv, keep), _mlx4(w.z, keep),
+                             _mlx4(w.a, keep), _mlx4(w.b, keep), _mlx4(w.out, keep),
+                             _c(c.conv_w, np.uint16), _c(c.A_log, np.float32),
+                             _c(c.dt_bias, np.uint16), _c(c.norm_w, np.uint16))
+    if rc != 0:
+        raise RuntimeError("orc_lin_chunk failed")
     return st
 

@@ -408,3 +408,34 @@ int orc_lin_step(int k_heads, int v_heads, int kd, int vd, int max_tokens, int t
     free(o);
     return rc;
 }
+
+int orc_gqa_chunk(int heads, int kv_heads, int kh, int max_tokens, float *kv_layer, int t0,
+                  int B, int hidden, float *states, const uint16_t *in_norm, const OrcMlx4 *wq,
+                  const OrcMlx4 *wk, const OrcMlx4 *wv, const OrcMlx4 *wo,
+                  const uint16_t *qn_w, const uint16_t *kn_w) {
+    if (B < 1 || t0 < 0) return -1;                  /* :1162-1163 */
+    for (int b = 0; b < B; b++) {
+        const int rc = orc_gqa_step(heads, kv_heads, kh, max_tokens, kv_layer, t0 + b, hidden,
+                                    states + (size_t)b * hidden, in_norm, wq, wk, wv, wo, qn_w,
+                                    kn_w);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+
+int orc_lin_chunk(int k_heads, int v_heads, int kd, int vd, int max_tokens, int t0, int B,
+                  int hidden, float *conv_ring, float *S, float *states,
+                  const uint16_t *in_norm, const OrcMlx4 *wqkv, const OrcMlx4 *wz,
+                  const OrcMlx4 *wa, const OrcMlx4 *wb, const OrcMlx4 *wout,
+                  const uint16_t *conv_w, const float *A_log, const uint16_t *dt_bias,
+                  const uint16_t *norm_w) {
+    if (B < 1 || t0 < 0) return -1;
+    for (int b = 0; b < B; b++) {                    /* token order, :1088-1109 */
+        const int rc = orc_lin_step(k_heads, v_heads, kd, vd, max_tokens, t0 + b, hidden,
+                                    conv_ring, S, states + (size_t)b * hidden, in_norm, wqkv, wz,
+                                    wa, wb, wout, conv_w, A_log, dt_bias, norm_w);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}
+

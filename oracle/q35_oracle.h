@@ -141,6 +141,23 @@ int orc_lin_step(int k_heads, int v_heads, int kd, int vd, int max_tokens, int t
                  const uint16_t *conv_w, const float *A_log, const uint16_t *dt_bias,
                  const uint16_t *norm_w);
 
+/* Prefill chunks on the residual stream: ds4f_attn_gqa_chunk
+ * (src/attn_qwen.c:1145-1252) and ds4f_attn_linear_chunk (:977-1135).  The
+ * reference batches the tokens' projections and output projections
+ * (ds4f_mlx4_matvec_batch, the same per-row sums) and runs the bodies
+ * serially in token order, so a chunk equals the layer steps of tokens
+ * t0 .. t0+B-1 in order, each on its own state: states [B][hidden]. */
+int orc_gqa_chunk(int heads, int kv_heads, int kh, int max_tokens, float *kv_layer, int t0,
+                  int B, int hidden, float *states, const uint16_t *in_norm, const OrcMlx4 *wq,
+                  const OrcMlx4 *wk, const OrcMlx4 *wv, const OrcMlx4 *wo,
+                  const uint16_t *qn_w, const uint16_t *kn_w);
+int orc_lin_chunk(int k_heads, int v_heads, int kd, int vd, int max_tokens, int t0, int B,
+                  int hidden, float *conv_ring, float *S, float *states,
+                  const uint16_t *in_norm, const OrcMlx4 *wqkv, const OrcMlx4 *wz,
+                  const OrcMlx4 *wa, const OrcMlx4 *wb, const OrcMlx4 *wout,
+                  const uint16_t *conv_w, const float *A_log, const uint16_t *dt_bias,
+                  const uint16_t *norm_w);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,8 +4,13 @@ MI355X): ds4f_gpu_attn_step against the oracle's layer steps
 linear_step :837-968).  input_layernorm, the MLX 4-bit projections, the
 core, the output projection and the residual all run on the device.
 
-Tolerance: max |gpu - oracle| <= 2e-3 on the hidden state after every layer
-(the path's bar for outputs); the relative RMS is printed beside it.
+Tolerance: the path's bar of 2e-3 on outputs, applied to the hidden state
+after every layer element by element relative to its magnitude above 1:
+|gpu - oracle| <= 2e-3 * max(1, |oracle|).  The state is fp32 of magnitude up
+to about 5 (a residual stream, not a bf16-stored attention output); the
+device keeps the KV cache in bf16 and the prefill attention's operands in
+fp16, whose roundings reach the state through the output projection.  The
+relative RMS is printed beside every check.
 """
 import sys
 
@@ -13,6 +18,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from ds4f_hip import synth as SY
 from ds4f_hip import workloads as W
 from ds4f_hip.attn import GpuAttention, KvCache
 
@@ -30,8 +36,9 @@ def _say(msg):
 
 
 def _err(got, ref):
+    """(max |d| / max(1, |ref|) elementwise, relative RMS)"""
     got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    mx = float(np.abs(got - ref).max())
+    mx = float((np.abs(got - ref) / np.maximum(1.0, np.abs(ref))).max())
     rr = float(np.sqrt(((got - ref) ** 2).sum() / max((ref ** 2).sum(), 1e-300)))
     return mx, rr
 
@@ -81,7 +88,7 @@ def test_single_layer_steps(kind):
             st_g = ga.attn_step(0, tok, st_g)
             st_o = _oracle_layer(kind, ref[0], ws[0], tok, st_o)
             mx, rr = _err(st_g, st_o)
-            _say(f"  max|err| {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"  max scaled err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
     finally:
         ga.close()
@@ -101,7 +108,7 @@ def test_four_layer_stack_three_tokens():
                 st_g = ga.attn_step(L, tok, st_g)
                 st_o = _oracle_layer(k, ref[L], ws[L], tok, st_o)
             mx, rr = _err(st_g, st_o)
-            _say(f"stack token {tok}: max|err| {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"stack token {tok}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
         # the device state agrees with the oracle's after the steps; the
         # ring holds raw projection rows, equal up to the matvecs' fp32
@@ -165,7 +172,42 @@ def test_step_graph_replays_match_oracle():
             for Lr, k in enumerate(kinds):
                 st_o = _oracle_layer(k, ref[Lr], ws[Lr], n_past + s, st_o)
             mx, rr = _err(got, st_o)
-            _say(f"graph replay token {n_past + s}: max|err| {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"graph replay token {n_past + s}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+    finally:
+        ga.close()
+
+
+@pytest.mark.parametrize("kind,t0,B", [(2, 0, 70), (2, 37, 100), (1, 0, 1), (1, 37, 100)])
+def test_chunk_matches_oracle(kind, t0, B):
+    """A prefill chunk of B tokens on the device (norm, 4-bit projections as
+    one MFMA GEMM, the prefill core, output GEMM + residual) against the
+    oracle's chunk (the per-token layer steps in order), then two decode
+    steps on the state the chunk left behind."""
+    ga, ref, ws = _stack([kind], t0, t0, 256)
+    try:
+        states = np.stack([W.hidden_state(HID, 0, 700 + b) for b in range(B)])
+        _say(f"chunk kind {kind} t0 {t0} B {B}")
+        got = ga.attn_chunk(0, t0, states)
+        if kind == 2:
+            exp = O.gqa_chunk(ref[0], t0, states, ws[0], GQ.heads, GQ.kv_heads, GQ.head_dim)
+        else:
+            ring, S = ref[0]
+            exp = O.lin_chunk(ring, S, t0, states, ws[0], LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+        mx, rr = _err(got, exp)
+        _say(f"  chunk max scaled err {mx:.3e} rel-rms {rr:.3e}")
+        assert mx <= ATOL
+        if kind == 2:
+            # the device cache holds the chunk's k / v rows in bf16: the
+            # oracle's decode steps read the same rows
+            ref[0][t0:t0 + B] = SY.bf16_round(ref[0][t0:t0 + B])
+        st_g = st_o = W.hidden_state(HID, 0, 901)
+        for s in range(2):
+            tok = t0 + B + s
+            st_g = ga.attn_step(0, tok, st_g)
+            st_o = _oracle_layer(kind, ref[0], ws[0], tok, st_o)
+            mx, rr = _err(st_g, st_o)
+            _say(f"  decode after chunk, token {tok}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
     finally:
         ga.close()
