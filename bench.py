@@ -43,6 +43,11 @@ Other workloads (one JSON line each, same fields):
                 the residual add: ds4f_hip_attn_step_async), 697 MB of
                 synthetic 4-bit weights; one HIP graph per step; HBM
                 roofline over the whole step's algorithmic bytes.
+  block_prefill a prefill of --tokens (4096) tokens from position 0 through
+                the same 40 whole layers, one chunk per layer
+                (ds4f_hip_attn_chunk_async: 4-bit projections as dequant
+                MFMA GEMMs); one HIP graph per pass; MFMA roofline over the
+                pass's algorithmic flops.
 """
 from __future__ import annotations
 
@@ -92,7 +97,7 @@ def main() -> int:
                                                                     "lin_prefill", "hbm_copy",
                                                                     "gqa_decode", "lin_decode",
                                                                     "mlx4_head",
-                                                                    "block_decode"])
+                                                                    "block_decode", "block_prefill"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     ap.add_argument("--npast", type=int, default=4096, help="cached positions (gqa_decode)")
     ap.add_argument("--rotate", type=int, default=0,
@@ -115,6 +120,8 @@ def main() -> int:
         return run_mlx4_head(args)
     if args.workload == "block_decode":
         return run_block_decode(args)
+    if args.workload == "block_prefill":
+        return run_block_prefill(args)
     return run_stack_decode(args)
 
 
@@ -824,6 +831,50 @@ def mlx4_bytes(R: int, C: int) -> int:
     return R * C // 2 + 2 * (R * C // 64) * 2
 
 
+def register_block_weights(ga, kinds, H: int, seed: int, dev, keep: bool):
+    """Synthetic MLX 4-bit layer weights for a stack: random nibbles,
+    per-group scales in the projections' range and biases that centre each
+    group, drawn on the device (torch generator seeded with seed) and
+    registered per layer.  Returns (weights per layer if keep, total weight
+    bytes, matrix MACs per token over the stack)."""
+    import numpy as np
+    import torch
+
+    from ds4f_hip import workloads as W
+    gq, lg = W.GqaGeom(), W.LinGeom()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    lo, hi = W.PROJ_SCALE
+
+    def m4(R, C):
+        n, ng = R * C, R * C // 64
+        vals = torch.randint(0, 256, (n // 2,), dtype=torch.uint8, device=dev, generator=gen)
+        sc = torch.rand(ng, device=dev, generator=gen) * (hi - lo) + lo
+        bi = -sc * (torch.rand(ng, device=dev, generator=gen) * 3.0 + 6.0)
+        u16 = lambda t: t.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+        return W.Mlx4W(vals.cpu().numpy().view(np.uint32), u16(sc), u16(bi), R, C)
+
+    weights, weight_bytes, macs = {}, 0, 0
+    for Lr, kd in enumerate(kinds):
+        in_norm = W.norm_weight(H, seed, Lr)
+        if kd == 2:
+            qn, kn = W.gqa_weights(gq, seed, Lr)
+            w = W.GqaLayerW(in_norm, m4(gq.heads * 2 * gq.head_dim, H),
+                            m4(gq.kv_heads * gq.head_dim, H), m4(gq.kv_heads * gq.head_dim, H),
+                            m4(H, gq.heads * gq.head_dim), qn, kn)
+            mats = (w.q, w.k, w.v, w.o)
+        else:
+            w = W.LinLayerW(in_norm, m4(lg.rows, H), m4(lg.v_heads * lg.vd, H), m4(lg.v_heads, H),
+                            m4(lg.v_heads, H), m4(H, lg.v_heads * lg.vd), W.lin_weights(lg, seed, Lr))
+            mats = (w.qkv, w.z, w.a, w.b, w.out)
+        ga.set_layer_weights(Lr, w)
+        weight_bytes += sum(mlx4_bytes(m.rows, m.cols) for m in mats)
+        macs += sum(m.rows * m.cols for m in mats)
+        if keep:
+            weights[Lr] = w
+    return weights, weight_bytes, macs
+
+
 def run_block_decode(args) -> int:
     import numpy as np
     import torch
@@ -856,38 +907,7 @@ def run_block_decode(args) -> int:
             L.check(lib.ds4f_hip_synth_conv_history(Lr, N, seed, S.tid(S.LIN_CONVSTATE, Lr),
                                                     None), "synth conv")
 
-    # synthetic 4-bit weights: random nibbles, per-group scales in the
-    # projections' range and biases that centre each group, drawn on the
-    # device (torch generator seeded with --seed) and registered per layer
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(seed)
-    lo, hi = W.PROJ_SCALE
-
-    def m4(R, C):
-        n, ng = R * C, R * C // 64
-        vals = torch.randint(0, 256, (n // 2,), dtype=torch.uint8, device=dev, generator=gen)
-        sc = torch.rand(ng, device=dev, generator=gen) * (hi - lo) + lo
-        bi = -sc * (torch.rand(ng, device=dev, generator=gen) * 3.0 + 6.0)
-        u16 = lambda t: t.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
-        return W.Mlx4W(vals.cpu().numpy().view(np.uint32), u16(sc), u16(bi), R, C)
-
-    weights, weight_bytes = {}, 0
-    for Lr, kd in enumerate(kinds):
-        in_norm = W.norm_weight(H, seed, Lr)
-        if kd == 2:
-            qn, kn = W.gqa_weights(gq, seed, Lr)
-            w = W.GqaLayerW(in_norm, m4(gq.heads * 2 * gq.head_dim, H),
-                            m4(gq.kv_heads * gq.head_dim, H), m4(gq.kv_heads * gq.head_dim, H),
-                            m4(H, gq.heads * gq.head_dim), qn, kn)
-            mats = (w.q, w.k, w.v, w.o)
-        else:
-            w = W.LinLayerW(in_norm, m4(lg.rows, H), m4(lg.v_heads * lg.vd, H), m4(lg.v_heads, H),
-                            m4(lg.v_heads, H), m4(H, lg.v_heads * lg.vd), W.lin_weights(lg, seed, Lr))
-            mats = (w.qkv, w.z, w.a, w.b, w.out)
-        ga.set_layer_weights(Lr, w)
-        weight_bytes += sum(mlx4_bytes(m.rows, m.cols) for m in mats)
-        if want_cpu:
-            weights[Lr] = w
+    weights, weight_bytes, _ = register_block_weights(ga, kinds, H, seed, dev, want_cpu)
     states = torch.empty((T, H), dtype=torch.float32, device=dev)
     for s in range(T):
         L.check(lib.ds4f_hip_synth(dptr(states[s]), H, 0, 0, 0.0, 1.0, seed,
@@ -976,6 +996,134 @@ def run_block_decode(args) -> int:
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
+
+def run_block_prefill(args) -> int:
+    """A prefill of --tokens tokens from position 0 through the 40 whole
+    layers: per layer one chunk (ds4f_hip_attn_chunk_async: input norm and
+    fp16 hi/lo split, the MLX 4-bit projections as one dequant MFMA GEMM,
+    the prefill core, the output GEMM accumulating into the states).  One
+    step = restore the input states (a 32 MB device copy) + the 40 chunks,
+    replayed as one HIP graph."""
+    import numpy as np
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip import synth as S
+    from ds4f_hip import workloads as W
+    from ds4f_hip.attn import GpuAttention, KvCache, dptr
+
+    lib = L.load()
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    gq, lg = W.GqaGeom(), W.LinGeom()
+    H = 2048
+    kinds = W.stack_kinds(40)
+    T, K, WU, seed = args.tokens, args.steps, args.warmup, args.seed
+    max_tokens = T + 64
+    want_cpu = not args.no_cpu_baseline
+
+    cache = KvCache(40, max_tokens) if want_cpu else None
+    ga = GpuAttention(kinds, max_tokens, cache)
+    weights, weight_bytes, macs = register_block_weights(ga, kinds, H, seed, dev, want_cpu)
+    states0 = torch.empty((T, H), dtype=torch.float32, device=dev)
+    L.check(lib.ds4f_hip_synth(dptr(states0), T * H, 0, 0, 0.0, 1.0, seed,
+                               S.tid(S.BLK_STATE, 0, 0), None), "synth states")
+    states = states0.clone()
+    torch.cuda.synchronize()
+
+    def launch_step(stream):
+        states.copy_(states0)
+        for Lr in range(40):
+            L.check(lib.ds4f_hip_attn_chunk_async(Lr, 0, T, dptr(states), stream),
+                    f"layer {Lr} chunk")
+
+    # first pass eagerly: it sizes the workspaces, which the graph reuses
+    launch_step(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        launch_step(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    for _ in range(WU):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(K):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    ev_sec = ev0.elapsed_time(ev1) * 1e-3
+    del graph
+    if not bool(torch.isfinite(states).all()):
+        raise RuntimeError("block_prefill: non-finite hidden state")
+
+    # algorithmic flops of one pass: the 4-bit matrices at 2 flops per MAC
+    # and token, the causal GQA attention, the chunked delta rule
+    gemm_flops = 2.0 * macs * T
+    gqa_flops = 10 * 4.0 * gq.heads * gq.head_dim * T * (T + 1) / 2
+    lin_flops = 30 * lin_prefill_flops(T)
+    flops = gemm_flops + gqa_flops + lin_flops
+    tflops = flops / (ev_sec / K) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "whole pass: 40 x (xprep + mlx4 dequant GEMM + prefill core + xprep + "
+                          "mlx4 dequant GEMM); peak is the fp16 one, the delta-rule core runs "
+                          "on fp32 MFMA",
+                "launches": K, "us_per_launch": round(ev_sec / K * 1e6, 2),
+                "flops_per_launch": flops, "gemm_flops": gemm_flops, "gqa_flops": gqa_flops,
+                "lin_flops": lin_flops}
+
+    cpu = None
+    if want_cpu:
+        # the reference's chunk runs the layer steps of the tokens in order;
+        # time all 40 layer steps at positions spread over the prefill (on
+        # the caches the device pass left) and integrate the linear fit
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        O.lib()
+        ga.sync(-1, to_host=True, n_kv_tokens=T)
+        st_host = states0.cpu().numpy()
+        pos = np.linspace(0, T - 1, 6).astype(int)
+        secs = []
+        for t in pos:
+            st = st_host[t].copy()
+            c0 = time.perf_counter()
+            for Lr, kd in enumerate(kinds):
+                if kd == 2:
+                    st = O.gqa_step(cache.kv[Lr], int(t), st, weights[Lr], gq.heads, gq.kv_heads,
+                                    gq.head_dim)
+                else:
+                    st = O.lin_step(cache.conv[Lr], cache.lin[Lr], int(t), st, weights[Lr],
+                                    lg.k_heads, lg.v_heads, lg.kd, lg.vd)
+            secs.append(time.perf_counter() - c0)
+        a, b = np.polyfit(pos.astype(float), np.array(secs), 1)
+        est = float(sum(a * t + b for t in range(T)))
+        cpu = {"value": round(T / est, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"C oracle (gcc -O2, 1 thread) 40 whole layer steps at {len(pos)} "
+                         f"positions 0..{T - 1} ({sum(secs):.1f} s), linear fit integrated "
+                         f"over the {T} serial steps of the reference's chunk (est. {est:.0f} s)"}
+
+    ga.close()
+    line = {"metric": f"attention-block prefill tokens/s ({T} tokens, 40 layers, projections "
+                      "included), 1 GPU",
+            "value": round(T * K / ev_sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
+            "warmup": WU, "ms_per_step": round(ev_sec / K * 1e3, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "mlx4-weights/fp16-mfma/fp32",
+            "data": "synthetic (MLX 4-bit weights from a seeded torch generator, hidden N(0,1))",
+            "config": {"workload": "qwen3.5-35b-a3b attention layers on the residual stream, "
+                                   "prefill: 40 layers (30 gated delta-rule + 10 GQA), input "
+                                   "norm, 4-bit projections, core, output projection, residual",
+                       "tokens": T, "t0": 0, "layers": 40, "hidden": H,
+                       "weight_bytes": weight_bytes, "graph_per_step": True},
+            "wall_ms_per_step": round(sec / K * 1e3, 4),
+            "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
 
 if __name__ == "__main__":
     sys.exit(main())

@@ -885,8 +885,7 @@ typedef struct LayerW {
     Q35Mlx4 out;               /* output projection: x, y set per call */
     const uint16_t *qn, *kn, *conv_w, *dt_bias, *norm_w;
     const float *A_log;
-    Q35Mlx4GemmJob *gjobs;     /* device: the chunk GEMMs' projections, then the output */
-    int gmax;                  /* widest projection */
+    Q35Mlx4GemmJob gj[5];      /* the chunk GEMMs' projections, then the output (y set per call) */
 } LayerW;
 
 /* activations between the launches of one layer step, floats */
@@ -1031,19 +1030,20 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
         outw = &w->out;
     }
     Part pt[40];
-    const void *pv[5], *ps[5], *pb[5], *psb[5], *in_norm, *jobs, *gjobs, *t0, *t1, *t2, *t3;
+    const void *pv[5], *ps[5], *pb[5], *psb[5], *in_norm, *jobs, *t0, *t1, *t2, *t3;
     int n = 0;
     for (int i = 0; i < np; i++) n += mlx4_parts(pt + n, proj[i], &pv[i], &ps[i], &pb[i]);
     n += mlx4_parts(pt + n, outw, &pv[4], &ps[4], &pb[4]);
-    /* (s, b - 1024 s) per row and 64-column group of each weight, for the
+    /* (16 s, b - 16 s) per row and 64-column group of each weight, for the
      * chunk GEMMs (filled on the device below) */
     for (int i = 0; i < 5; i++) {
         const Ds4fGpuMlx4W *m = i < 4 ? (i < np ? proj[i] : NULL) : outw;
-        pt[n++] = (Part){NULL, m ? (size_t)m->rows * (m->cols / 64) * sizeof(Q35Mlx4SB) : 0, &psb[i]};
+        pt[n++] = (Part){NULL,
+                         m ? (size_t)q35_mlx4_sb_npad(m->rows) * (m->cols / 64) * sizeof(Q35Mlx4SB) : 0,
+                         &psb[i]};
     }
     pt[n++] = (Part){w->in_norm, w->in_norm ? (size_t)hidden * 2 : 0, &in_norm};
     pt[n++] = (Part){NULL, (size_t)np * sizeof(Q35Mlx4Job), &jobs};   /* filled below */
-    pt[n++] = (Part){NULL, (size_t)(np + 1) * sizeof(Q35Mlx4GemmJob), &gjobs};
     if (kind == DS4F_LAYER_GQA) {
         pt[n++] = (Part){w->q_norm, GQA_D * 2, &t0};
         pt[n++] = (Part){w->k_norm, GQA_D * 2, &t1};
@@ -1075,32 +1075,22 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
     }
     lw->jobs = (Q35Mlx4Job *)jobs;
     lw->njobs = np;
-    /* the chunk GEMMs' job table: the np projections, then the output */
-    Q35Mlx4GemmJob gj[5];
+    /* the chunk GEMMs' jobs: the np projections, then the output */
     int ng = 0;
-    lw->gmax = 0;
     for (int i = 0; i < 5; i++) {
         const Ds4fGpuMlx4W *m = i < 4 ? (i < np ? proj[i] : NULL) : outw;
         if (!m) continue;
         if (q35_mlx4_sb((const uint16_t *)ps[i], (const uint16_t *)pb[i], (Q35Mlx4SB *)psb[i],
-                        (int64_t)m->rows * (m->cols / 64), P.stream) != hipSuccess ||
+                        m->rows, m->cols / 64, P.stream) != hipSuccess ||
             hipStreamSynchronize(P.stream) != hipSuccess) {
             set_err("layer weights: scale table failed");
             hipFree(lw->d);
             memset(lw, 0, sizeof *lw);
             return -1;
         }
-        gj[ng++] = (Q35Mlx4GemmJob){(const uint32_t *)pv[i], (const Q35Mlx4SB *)psb[i], m->rows};
-        if (i < 4 && m->rows > lw->gmax) lw->gmax = m->rows;
+        lw->gj[ng++] = (Q35Mlx4GemmJob){(const uint32_t *)pv[i], (const Q35Mlx4SB *)psb[i], NULL,
+                                        m->rows, 0};
     }
-    if (hipMemcpy((void *)gjobs, gj, (size_t)ng * sizeof(Q35Mlx4GemmJob), hipMemcpyHostToDevice) !=
-        hipSuccess) {
-        set_err("layer weights: GEMM job table upload failed");
-        hipFree(lw->d);
-        memset(lw, 0, sizeof *lw);
-        return -1;
-    }
-    lw->gjobs = (Q35Mlx4GemmJob *)gjobs;
     lw->in_norm = (const uint16_t *)in_norm;
     memset(&lw->out, 0, sizeof lw->out);
     lw->out.vals = (const uint32_t *)pv[4];
@@ -1213,26 +1203,25 @@ static size_t ch_kmax(void) {
     return k;
 }
 
-typedef struct { uint16_t *xh, *xl; float *xsum; float *out[CH_N]; } ChunkWs;
+typedef struct { uint16_t *xw; float *xsum; float *out[CH_N]; } ChunkWs;
 
 /* byte offsets of the workspace parts for mpad rows; the total when ws is
  * NULL, else ws filled with pointers into P.d_chunk */
 static size_t chunk_layout(int mpad, ChunkWs *ws) {
     const size_t K = ch_kmax();
-    size_t sizes[3 + CH_N], off[3 + CH_N], total = 0;
-    sizes[0] = sizes[1] = (size_t)mpad * K * 2;
-    sizes[2] = (K / 64) * (size_t)mpad * 4;
-    for (int i = 0; i < CH_N; i++) sizes[3 + i] = (size_t)mpad * ch_width(i) * 4;
-    for (int i = 0; i < 3 + CH_N; i++) {
+    size_t sizes[2 + CH_N], off[2 + CH_N], total = 0;
+    sizes[0] = (size_t)mpad * K * 4;            /* fp16 hi and lo */
+    sizes[1] = (K / 64) * (size_t)mpad * 4;
+    for (int i = 0; i < CH_N; i++) sizes[2 + i] = (size_t)mpad * ch_width(i) * 4;
+    for (int i = 0; i < 2 + CH_N; i++) {
         off[i] = total;
         total += (sizes[i] + 255) & ~(size_t)255;
     }
     if (ws) {
         char *b = (char *)P.d_chunk;
-        ws->xh = (uint16_t *)(b + off[0]);
-        ws->xl = (uint16_t *)(b + off[1]);
-        ws->xsum = (float *)(b + off[2]);
-        for (int i = 0; i < CH_N; i++) ws->out[i] = (float *)(b + off[3 + i]);
+        ws->xw = (uint16_t *)(b + off[0]);
+        ws->xsum = (float *)(b + off[1]);
+        for (int i = 0; i < CH_N; i++) ws->out[i] = (float *)(b + off[2 + i]);
     }
     return total;
 }
@@ -1254,28 +1243,28 @@ static int ensure_chunk(int B, ChunkWs *ws) {
     return 0;
 }
 
-/* X = [norm](x rows), then y = X W^T for the njobs GEMM jobs of a device
- * job table, job j writing ys[j] [B][lds[j]] */
+/* X = [norm](x rows), then y = X W^T for the njobs GEMM jobs, job j
+ * writing ys[j] [B][lds[j]] */
 static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, int B,
-                      const Q35Mlx4GemmJob *jobs, int njobs, int max_n, float *const *ys,
-                      const int *lds, int accumulate, const ChunkWs *ws, hipStream_t st) {
-    Q35Mlx4Xprep xp = {x, norm_w, ws->xh, ws->xl, ws->xsum, B, P.chunk_cap, K, ldx};
+                      const Q35Mlx4GemmJob *jobs, int njobs, float *const *ys, const int *lds,
+                      int accumulate, const ChunkWs *ws, hipStream_t st) {
+    Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, P.chunk_cap, K, ldx};
     HIPCHK(q35_mlx4_xprep(&xp, st));
     Q35Mlx4Gemm g;
     memset(&g, 0, sizeof g);
-    g.xh = ws->xh;
-    g.xl = ws->xl;
+    g.xw = ws->xw;
     g.xsum = ws->xsum;
-    g.jobs = jobs;
     for (int j = 0; j < njobs; j++) {
-        g.y[j] = ys[j];
-        g.ldy[j] = lds[j];
+        g.jobs[j] = jobs[j];
+        g.jobs[j].y = ys[j];
+        g.jobs[j].ldy = lds[j];
     }
+    g.njobs = njobs;
     g.M = B;
     g.Mpad = P.chunk_cap;
     g.K = K;
     g.accumulate = accumulate;
-    HIPCHK(q35_mlx4_gemm(&g, njobs, max_n, st));
+    HIPCHK(q35_mlx4_gemm(&g, st));
     return 0;
 }
 
@@ -1311,8 +1300,7 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
         ys[j] = ws.out[outs[j]];
         lds[j] = (int)ch_width(outs[j]);
     }
-    if (chunk_gemm(states, H, lw->in_norm, H, B, lw->gjobs, lw->njobs, lw->gmax, ys, lds, 0, &ws,
-                   st) != 0)
+    if (chunk_gemm(states, H, lw->in_norm, H, B, lw->gj, lw->njobs, ys, lds, 0, &ws, st) != 0)
         return -1;
     /* the core over the chunk */
     int core_out;
@@ -1332,7 +1320,7 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
     float *yo[1] = {states};
     const int ldo[1] = {H};
     return chunk_gemm(ws.out[core_out], (int)ch_width(core_out), NULL, (int)ch_width(core_out), B,
-                      lw->gjobs + lw->njobs, 1, H, yo, ldo, 1, &ws, st);
+                      lw->gj + lw->njobs, 1, yo, ldo, 1, &ws, st);
 }
 
 int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {

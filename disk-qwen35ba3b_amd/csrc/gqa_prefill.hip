@@ -245,27 +245,8 @@ __device__ __forceinline__ float half_pair_max(float v) {
     return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
 }
 
-/* s_waitcnt vmcnt(0) (expcnt and lgkmcnt left open): this wave's direct-to-
- * LDS loads have landed */
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-/* One direct-to-LDS load: 16 bytes a lane from buffer offset soff + voff
- * (range-checked) to LDS byte lds + 16 * lane.  Issued as inline assembly
- * so the compiler's wait insertion does not see it: it cannot tell LDS
- * stages apart and would wait for every staging load in flight before the
- * next LDS read.  The kernel orders these loads itself (wait_dma() before
- * each barrier); loads the compiler does not count can only make its own
- * load waits stricter. */
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"   /* m0 is reserved; nothing else here uses it */
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff,
-                                      uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
+/* this wave's direct-to-LDS loads have landed */
+__device__ __forceinline__ void wait_dma() { q35_wait_vm<0>(); }
 
 /* q block qb's output rows of this wave: O / l times sigmoid(gate), fp32 */
 __device__ __forceinline__ void store_rows(const Q35GqaPrefill &p, int g, int qb, int hl, int col,
@@ -368,7 +349,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int j = wg + 4 * i;
-            dma16(part ? vrs : krs, base + j * 1024, dma_lane, so + j * 1024);
+            q35_dma16(part ? vrs : krs, base + j * 1024, dma_lane, so + j * 1024);
         }
     };
 

@@ -7,29 +7,42 @@
  *
  * Exactness.  With w = q s + b (q in 0..15, s and b the BF16 scale and
  * bias of the 64-element group), and G the groups along K,
- *     y[m][n] = sum_g s[n,g] sum_{k in g} (1024 + q) x  +  b'[n,g] xsum[m,g],
- *     b' = b - 1024 s,  xsum[m,g] = sum_{k in g} x.
- * 1024 + q is exact in fp16, x is carried as an fp16 hi + lo pair (about
- * 22 bits), each MFMA product is exact in fp32, and the group partial is
- * scaled by s in fp32 after its 8 MFMAs (4 k-steps x hi / lo); xsum is the
- * sum of the same hi + lo values, so the 1024 terms cancel to fp32
- * rounding.  The result differs from the reference's fp32 dot products by
- * fp32 rounding of the group sums.
+ *     y[m][n] = sum_g s'[n,g] sum_{k in g} (1 + q/16) x  +  b'[n,g] xsum[m,g],
+ *     s' = 16 s,  b' = b - 16 s,  xsum[m,g] = sum_{k in g} x.
+ * 1 + q/16 is exact in fp16 (the nibble in mantissa bits 6..9 under the
+ * exponent of 1), x is carried as an fp16 hi + lo pair (about 22 bits),
+ * each MFMA product is exact in fp32, and the group partial is scaled by
+ * s' in fp32 after its 8 MFMAs (4 k-steps x hi / lo); xsum is the sum of
+ * the same hi + lo values.  The offset 1 is at most about twice the q/16
+ * part, so the cancellation against b' xsum costs about a bit, and the
+ * result differs from the reference's fp32 dot products by fp32 rounding
+ * of the group sums.
  *
- * Layouts (written by xprep_kernel):
- *   xh, xl  fp16 [Mpad][K]: 8 consecutive k (one nibble word's worth) kept
- *           in the order 0,4,1,5,2,6,3,7, the order in which a word's
- *           nibbles become fp16 pairs ((w >> 4j) & 0x000F000F | 0x64006400
- *           gives 1024 + q_j and 1024 + q_{j+4});
- *   xsum    fp32 [G][Mpad].
+ * Layouts:
+ *   xw      (xprep_kernel) per 64-token tile mt and group g, a 16 KB block
+ *           at ((mt G + g) 2 + {0: hi, 1: lo}) 8 KB: 64 rows of 128 bytes,
+ *           fp16, 8 consecutive k (one nibble word's worth) kept in the
+ *           order 0,4,1,5,2,6,3,7, the order in which a word's nibbles become
+ *           fp16 pairs (nibbles j and j + 4 moved to bits 6..9 and 22..25,
+ *           ORed into 0x3C003C00, give 1 + q_j / 16 and 1 + q_{j+4} / 16);
+ *           word j of row r at 16-byte slot
+ *           j ^ (r & 7) ^ ((r >> 3) & 1), so that the MFMA operand reads
+ *           (32 rows, one word each) hit distinct LDS banks;
+ *   xsum    fp32 [G][Mpad];
+ *   sb      (sb_kernel) (16 s, b - 16 s) as [G][Npad], Npad = N rounded up
+ *           to 256, zeros past N;
+ *   weights the MLX words as they are, [N][K/8].
  * In a group (8 words), MFMA k-step ks of lane half h is word 4h + ks: a
- * lane's weight operand for a whole group is one 16-byte load.
+ * lane's weight operand for a whole group is one 16-byte read.
  *
  * gemm_kernel: 256 threads, a 64-token x 256-feature tile; wave w owns
- * features 64w..64w+63 as 2 x 2 blocks of v_mfma_f32_32x32x16_f16 (A = X
- * from LDS, B = W^T converted in registers).  X tiles of one group (hi, lo,
- * xsum) are staged through LDS, double-buffered, the next group's X and
- * weights in registers meanwhile.
+ * features 64w..64w+63 as 2 x 2 blocks of v_mfma_f32_32x32x16_f16 (A = X,
+ * B = W^T converted in registers).  Every global load is a direct-to-LDS
+ * load into a ring of three stages, one group each (X hi and lo 16 KB,
+ * the tile's weight words 8 KB, (s, b') 2 KB, xsum 256 B), issued two
+ * groups ahead; each wave waits for its own loads of the next group
+ * before the one barrier a group.  Two workgroups fit a CU (157.5 KB of
+ * LDS), two waves a SIMD.
  */
 #include "q35_device.h"
 #include "q35_launch.h"
@@ -41,14 +54,28 @@ namespace {
 constexpr int NT = 256;
 constexpr int MT = 64;                 /* tokens a tile */
 constexpr int NTILE = 256;             /* features a tile, 64 a wave */
-constexpr int XROW = 144;              /* LDS bytes of one token row of a group: 128 + 16 pad */
-constexpr float OFFSET = 1024.0f;      /* fp16 0x6400 */
+constexpr int XBLK = MT * 128;         /* bytes of a tile's hi (or lo) X of one group */
+constexpr int WBLK = NTILE * 32;       /* bytes of a tile's weight words of one group */
+constexpr int SBLK = NTILE * 8;        /* bytes of a tile's (s, b') of one group */
+constexpr int OFF_W = 2 * XBLK, OFF_SB = OFF_W + WBLK, OFF_XS = OFF_SB + SBLK;
+constexpr int STAGE = OFF_XS + MT * 4; /* 26880 bytes */
+constexpr int NSTAGE = 3;
+constexpr float QSTEP = 16.0f;         /* B = 1 + q / QSTEP */
 
 /* the word's order of k inside a group: slot j of word v holds k = 8v + PERM[j] */
 __device__ __forceinline__ int perm8(int j) { return (j >> 1) + 4 * (j & 1); }
 
-/* x rows -> (optional RMSNorm) -> fp16 hi / lo in word order, and the
- * group sums of hi + lo.  One workgroup per token row (rows >= M: zeros);
+/* 16-byte slot of word j of tile row r in its 128-byte X row; distinct
+ * over any 8 consecutive rows and, with the row's 128-byte half, over any
+ * 16: the operand reads are free of bank conflicts whether the LDS serves
+ * 8 lanes over 32 banks or 16 lanes over 64 banks a cycle */
+__device__ __forceinline__ int xslot(int r, int j) { return j ^ (r & 7) ^ ((r >> 3) & 1); }
+/* slot of half h (words 4h..4h+3) of tile feature row r in its 32-byte
+ * weight row, by the same argument over 4 and 8 consecutive rows */
+__device__ __forceinline__ int wslot(int r, int h) { return h ^ (((r >> 2) ^ (r >> 3)) & 1); }
+
+/* x rows -> (optional RMSNorm) -> fp16 hi / lo in word order, tiled, and
+ * the group sums of hi + lo.  One workgroup per token row (rows >= M: zeros);
  * thread t takes words t, t + 256, ... of the row. */
 __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
@@ -100,90 +127,128 @@ __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
             lo[j] = l;
             s += (float)h + (float)l;
         }
-        *reinterpret_cast<f16x8_t *>(p.xh + (size_t)m * p.K + 8 * v) = hi;
-        *reinterpret_cast<f16x8_t *>(p.xl + (size_t)m * p.K + 8 * v) = lo;
+        const int r = m & (MT - 1);
+        uint8_t *blk = reinterpret_cast<uint8_t *>(p.xw) +
+                       ((size_t)(m / MT) * (p.K / 64) + (v >> 3)) * 2 * XBLK + r * 128 +
+                       xslot(r, v & 7) * 16;
+        *reinterpret_cast<f16x8_t *>(blk) = hi;
+        *reinterpret_cast<f16x8_t *>(blk + XBLK) = lo;
         /* the group's 8 words are 8 consecutive threads of a wave */
         s = q35_sum8(s);
         if ((v & 7) == 0) p.xsum[(size_t)(v >> 3) * p.Mpad + m] = s;
     }
 }
 
-/* (s, b - 1024 s) per (row, group) of a weight, from its BF16 scales and
- * biases (biases may be NULL) */
-__global__ void sb_kernel(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int64_t n) {
+/* (16 s, b - 16 s) of a weight's rows and groups as [G][npad] (zeros for
+ * rows past N), from its BF16 scales and biases [N][G] (biases may be
+ * NULL) */
+__global__ void sb_kernel(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int N, int G,
+                          int npad) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float s = q35_bf2f(scales[i]);
-    const float b = biases ? q35_bf2f(biases[i]) : 0.0f;
-    sb[i] = Q35Mlx4SB{s, b - OFFSET * s};
+    if (i >= (int64_t)G * npad) return;
+    const int g = (int)(i / npad), n = (int)(i % npad);
+    float sv = 0.0f, bv = 0.0f;
+    if (n < N) {
+        const float s = q35_bf2f(scales[(size_t)n * G + g]);
+        const float b = biases ? q35_bf2f(biases[(size_t)n * G + g]) : 0.0f;
+        sv = QSTEP * s;
+        bv = b - sv;
+    }
+    sb[i] = Q35Mlx4SB{sv, bv};
 }
 
-/* a word's 8 nibbles as the fp16 B operand 1024 + q, in word order */
-__device__ __forceinline__ f16x8_t nib_f16(uint32_t w) {
+/* a word's 8 nibbles as the fp16 B operand 1 + q / 16, in word order:
+ * pair j (nibbles j and j + 4, bits 4j and 16 + 4j) shifted to bits 6 and
+ * 22, masked, ORed into the exponent of 1.  The mask and the exponent bits
+ * are held in registers (an SGPR and a VGPR) so that each pair is one
+ * shift and one v_and_or_b32. */
+__device__ __forceinline__ f16x8_t nib_f16(uint32_t w, uint32_t mask, uint32_t one) {
     u32x4_t u;
-#pragma unroll
-    for (int j = 0; j < 4; j++) u[j] = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+    u[0] = ((w << 6) & mask) | one;
+    u[1] = ((w << 2) & mask) | one;
+    u[2] = ((w >> 2) & mask) | one;
+    u[3] = ((w >> 6) & mask) | one;
     return __builtin_bit_cast(f16x8_t, u);
 }
 
+__device__ __forceinline__ int ntiles(int N) { return (N + NTILE - 1) / NTILE; }
+
+/* One workgroup per (job, 256-feature tile, 64-token tile), numbered with
+ * the token tile fastest over the jobs' feature tiles in order.  Work-
+ * groups are handed to the 8 XCDs in turn, so with 8 | token tiles an XCD
+ * holds token tiles of one residue mod 8 over consecutive feature tiles:
+ * about 8 x 8 tiles at once, sharing X and weight tiles in its L2. */
 __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
-    const Q35Mlx4GemmJob J = p.jobs[blockIdx.z];
-    float *const Y = p.y[blockIdx.z];
-    const int ldy = p.ldy[blockIdx.z];
-    const int n0 = blockIdx.x * NTILE, m0 = blockIdx.y * MT;
-    if (n0 >= J.N) return;                       /* a narrower job of the launch */
+    const int ntm = p.Mpad / MT;
+    const int mt = blockIdx.x % ntm;
+    int nt = blockIdx.x / ntm;
+    /* the job of feature tile nt (uniform selects: the job array is kernel
+     * arguments, not indexed memory) */
+    Q35Mlx4GemmJob J = p.jobs[0];
+#pragma unroll
+    for (int j = 1; j < Q35_GEMM_MAX_JOBS; j++) {
+        const int prev = ntiles(J.N);
+        if (j < p.njobs && nt >= prev) {
+            nt -= prev;
+            J = p.jobs[j];
+        }
+    }
+    float *const Y = J.y;
+    const int ldy = J.ldy;
+    const int n0 = nt * NTILE, m0 = mt * MT;
     const int t = threadIdx.x, lane = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int h = lane >> 5, c = lane & 31;
     const int G = p.K / 64;
+    const int npad = (J.N + NTILE - 1) / NTILE * NTILE;
 
-    __shared__ __align__(16) uint8_t sx[2][2][MT * XROW];   /* [buffer][hi, lo] */
-    __shared__ __align__(16) float sxs[2][MT];
+    __shared__ __align__(16) uint8_t smem[NSTAGE * STAGE];
+    const uint32_t lds0 = q35_lds_addr(smem);
 
-    /* weights: lane's rows n = n0 + 64w + 32nb + c, range-checked (rows past N
-     * read zero); group g of row n is 8 words at n * K / 8 + 8g, the lane's
-     * 4 at + 4h */
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(p.xw)), 0, (int)((size_t)p.Mpad * p.K * 4), Q35_BUF_DW3);
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         q35_uniform_ptr(const_cast<uint32_t *>(J.vals)), 0, (int)((size_t)J.N * p.K / 2), Q35_BUF_DW3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<Q35Mlx4SB *>(J.sb)), 0, (int)((size_t)J.N * G * 8), Q35_BUF_DW3);
-    int nrow[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; nb++) nrow[nb] = n0 + 64 * w + 32 * nb + c;
-    auto load_w = [&](int g, u32x4_t (&wq)[2], uint32_t (&sbv)[2][2]) {
-#pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
-            const int n = nrow[nb] < J.N ? nrow[nb] : J.N;      /* J.N: past the buffer */
-            wq[nb] = __builtin_amdgcn_raw_buffer_load_b128(wr, ((n * (p.K / 8) + 8 * g + 4 * h) * 4), 0, 0);
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(sr, (n * G + g) * 8, 0, 0);
-            sbv[nb][0] = v[0];
-            sbv[nb][1] = v[1];
-        }
-    };
-    /* X of a group: thread t moves 32 bytes of hi and of lo of token row t / 4 */
-    const int xr = t >> 2, xq = t & 3;
-    const __amdgpu_buffer_rsrc_t xhr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<uint16_t *>(p.xh)), 0, (int)((size_t)p.Mpad * p.K * 2), Q35_BUF_DW3);
-    const __amdgpu_buffer_rsrc_t xlr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<uint16_t *>(p.xl)), 0, (int)((size_t)p.Mpad * p.K * 2), Q35_BUF_DW3);
-    const __amdgpu_buffer_rsrc_t xsr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<Q35Mlx4SB *>(J.sb)), 0, (int)((size_t)G * npad * 8), Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t ssr = __builtin_amdgcn_make_buffer_rsrc(
         q35_uniform_ptr(const_cast<float *>(p.xsum)), 0, (int)((size_t)G * p.Mpad * 4), Q35_BUF_DW3);
-    const int xoff = ((m0 + xr) * p.K) * 2 + xq * 32;
-    auto load_x = [&](int g, u32x4_t (&xv)[4], uint32_t &xs) {
-        xv[0] = __builtin_amdgcn_raw_buffer_load_b128(xhr, xoff + g * 128, 0, 0);
-        xv[1] = __builtin_amdgcn_raw_buffer_load_b128(xhr, xoff + g * 128 + 16, 0, 0);
-        xv[2] = __builtin_amdgcn_raw_buffer_load_b128(xlr, xoff + g * 128, 0, 0);
-        xv[3] = __builtin_amdgcn_raw_buffer_load_b128(xlr, xoff + g * 128 + 16, 0, 0);
-        xs = __builtin_amdgcn_raw_buffer_load_b32(xsr, (g * p.Mpad + m0 + (t & 63)) * 4, 0, 0);
+
+    /* weight staging: load i (of 8, this wave's w and w + 4) puts 16-byte
+     * LDS position 64 i + lane, row r = position / 2 in slot position & 1,
+     * which holds half wslot(r, slot) of the row (wslot is its own inverse
+     * in h); rows past N read row N - 1, whose products no lane stores */
+    uint32_t wv[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int pos = 64 * (w + 4 * q) + lane, r = pos >> 1;
+        const int n = n0 + r < J.N ? n0 + r : J.N - 1;
+        wv[q] = (uint32_t)n * (uint32_t)(p.K / 2) + (uint32_t)wslot(r, pos & 1) * 16;
+    }
+    /* group g into stage st: X 16 loads, weights 8, (s, b') 2, xsum 1 (a
+     * dword load); waves 0-2 issue 7 of them, wave 3 issues 6 */
+    auto issue = [&](int g, int st) {
+        const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
+        const uint32_t xb = (uint32_t)(mt * G + g) * (2 * XBLK);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int i = w + 4 * q;
+            q35_dma16(xr, sb + i * 1024, lane * 16, xb + i * 1024);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+            q35_dma16(wr, sb + OFF_W + (w + 4 * q) * 1024, wv[q], (uint32_t)g * 32);
+        if (w < 2)
+            q35_dma16(sr, sb + OFF_SB + w * 1024, lane * 16, (uint32_t)(g * npad + n0) * 8 + w * 1024);
+        else if (w == 2)
+            q35_dma4(ssr, sb + OFF_XS, lane * 4, (uint32_t)(g * p.Mpad + m0) * 4);
     };
-    auto store_x = [&](int buf, const u32x4_t (&xv)[4], uint32_t xs) {
-        uint8_t *hb = &sx[buf][0][xr * XROW + xq * 32];
-        uint8_t *lb = &sx[buf][1][xr * XROW + xq * 32];
-        *reinterpret_cast<u32x4_t *>(hb) = xv[0];
-        *reinterpret_cast<u32x4_t *>(hb + 16) = xv[1];
-        *reinterpret_cast<u32x4_t *>(lb) = xv[2];
-        *reinterpret_cast<u32x4_t *>(lb + 16) = xv[3];
-        if (t < MT) sxs[buf][t] = __uint_as_float(xs);
+    /* this wave's loads of the group before the last issued have landed */
+    auto wait_prev = [&]() {
+        if (w == 3)
+            q35_wait_vm<6>();
+        else
+            q35_wait_vm<7>();
     };
 
     f32x16_t acc[2][2];
@@ -194,28 +259,41 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[mb][nb][i] = 0.0f;
 
-    u32x4_t wq[2], xv[4];
-    uint32_t sbv[2][2], xs;
-    load_w(0, wq, sbv);
-    load_x(0, xv, xs);
-    store_x(0, xv, xs);
+    issue(0, 0);
+    if (G > 1) {
+        issue(1, 1);
+        wait_prev();
+    } else {
+        q35_wait_vm<0>();
+    }
     q35_lds_barrier();
 
+    /* a wave whose 64 features all lie past N (a narrow job) only stages */
+    const bool idle = n0 + 64 * w >= J.N;
+    uint32_t mask, one;
+    asm("s_mov_b32 %0, 0x03c003c0" : "=s"(mask));
+    asm("v_mov_b32 %0, 0x3c003c00" : "=v"(one));
+
+    int st = 0;
     for (int g = 0; g < G; g++) {
-        const int buf = g & 1;
-        /* this group's operands in registers, the next group's requested */
+        if (g + 2 < G) issue(g + 2, st == 0 ? 2 : st - 1);
+        if (idle) goto next;
+        {
+        const uint8_t *S = smem + st * STAGE;
+        /* the weight operand: this lane's words 4h..4h+3 of rows
+         * 64w + 32nb + c, and their (s, b') */
         f16x8_t bf[2][4];
         float sc[2], bp[2];
 #pragma unroll
         for (int nb = 0; nb < 2; nb++) {
+            const int r = 64 * w + 32 * nb + c;
+            const u32x4_t wq = *reinterpret_cast<const u32x4_t *>(S + OFF_W + r * 32 + wslot(r, h) * 16);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) bf[nb][ks] = nib_f16(wq[nb][ks]);
-            sc[nb] = __uint_as_float(sbv[nb][0]);
-            bp[nb] = __uint_as_float(sbv[nb][1]);
+            for (int ks = 0; ks < 4; ks++) bf[nb][ks] = nib_f16(wq[ks], mask, one);
+            const float2 v = *reinterpret_cast<const float2 *>(S + OFF_SB + r * 8);
+            sc[nb] = v.x;
+            bp[nb] = v.y;
         }
-        const int gn = g + 1 < G ? g + 1 : g;
-        load_w(gn, wq, sbv);
-        load_x(gn, xv, xs);
 
         f32x16_t tmp[2][2];
 #pragma unroll
@@ -223,9 +301,10 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
             f16x8_t ah[2], al[2];
 #pragma unroll
             for (int mb = 0; mb < 2; mb++) {
-                const int off = (32 * mb + c) * XROW + (4 * h + ks) * 16;
-                ah[mb] = *reinterpret_cast<const f16x8_t *>(&sx[buf][0][off]);
-                al[mb] = *reinterpret_cast<const f16x8_t *>(&sx[buf][1][off]);
+                const int r = 32 * mb + c;
+                const int off = r * 128 + xslot(r, 4 * h + ks) * 16;
+                ah[mb] = *reinterpret_cast<const f16x8_t *>(S + off);
+                al[mb] = *reinterpret_cast<const f16x8_t *>(S + XBLK + off);
             }
 #pragma unroll
             for (int mb = 0; mb < 2; mb++)
@@ -243,12 +322,13 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
                 }
         }
         /* acc += s * partial + b' * xsum; lane rows 32mb + 8(i/4) + 4h + i%4 */
+        const float *xs = reinterpret_cast<const float *>(S + OFF_XS);
 #pragma unroll
         for (int mb = 0; mb < 2; mb++) {
             float xsv[16];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const float4 v = *reinterpret_cast<const float4 *>(&sxs[buf][32 * mb + 8 * q + 4 * h]);
+                const float4 v = *reinterpret_cast<const float4 *>(xs + 32 * mb + 8 * q + 4 * h);
                 xsv[4 * q] = v.x, xsv[4 * q + 1] = v.y, xsv[4 * q + 2] = v.z, xsv[4 * q + 3] = v.w;
             }
 #pragma unroll
@@ -257,12 +337,21 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
                 for (int i = 0; i < 16; i++)
                     acc[mb][nb][i] = fmaf(sc[nb], tmp[mb][nb][i], fmaf(bp[nb], xsv[i], acc[mb][nb][i]));
         }
-        /* the next group's X into the other buffer (its last readers passed
-         * the previous barrier) */
-        store_x(buf ^ 1, xv, xs);
+        }
+    next:
+        /* the next group's stage is complete for every wave; this one is
+         * free for the load issued next iteration */
+        if (g + 2 < G)
+            wait_prev();
+        else
+            q35_wait_vm<0>();
         q35_lds_barrier();
+        st = st == 2 ? 0 : st + 1;
     }
 
+    int nrow[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) nrow[nb] = n0 + 64 * w + 32 * nb + c;
     /* y[m][n] (+= with accumulate): lanes 0..31 of a row write 32
      * consecutive features */
 #pragma unroll
@@ -284,13 +373,16 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
 
 }  // namespace
 
-extern "C" hipError_t q35_mlx4_sb(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int64_t n,
-                                  hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
+extern "C" hipError_t q35_mlx4_sb(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int N,
+                                  int G, hipStream_t stream) {
+    if (N < 1 || G < 1) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)G * q35_mlx4_sb_npad(N);
     hipLaunchKernelGGL(sb_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, scales, biases, sb,
-                       n);
+                       N, G, q35_mlx4_sb_npad(N));
     return hipGetLastError();
 }
+
+extern "C" int q35_mlx4_sb_npad(int N) { return (N + NTILE - 1) / NTILE * NTILE; }
 
 extern "C" hipError_t q35_mlx4_xprep(const Q35Mlx4Xprep *p, hipStream_t stream) {
     if (p->K % 64 != 0 || p->K > 8192 || p->Mpad % MT != 0 || p->M > p->Mpad || p->M < 1)
@@ -299,13 +391,24 @@ extern "C" hipError_t q35_mlx4_xprep(const Q35Mlx4Xprep *p, hipStream_t stream) 
     return hipGetLastError();
 }
 
-extern "C" hipError_t q35_mlx4_gemm(const Q35Mlx4Gemm *p, int njobs, int max_n, hipStream_t stream) {
-    if (p->K % 64 != 0 || p->Mpad % MT != 0 || p->M > p->Mpad || njobs < 1 ||
-        njobs > Q35_GEMM_MAX_JOBS || max_n < 1 ||
-        (int64_t)max_n * p->K / 2 >= ((int64_t)1 << 31) || (int64_t)p->Mpad * p->K * 2 >= ((int64_t)1 << 31))
+extern "C" hipError_t q35_mlx4_gemm(const Q35Mlx4Gemm *p, hipStream_t stream) {
+    if (p->K < 64 || p->K % 64 != 0 || p->Mpad % MT != 0 || p->M > p->Mpad || p->M < 1 || p->njobs < 1 ||
+        p->njobs > Q35_GEMM_MAX_JOBS || (int64_t)p->Mpad * p->K * 4 >= ((int64_t)1 << 31) ||
+        (int64_t)(p->K / 64) * p->Mpad * 4 >= ((int64_t)1 << 31))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((max_n + NTILE - 1) / NTILE), (unsigned)(p->Mpad / MT), (unsigned)njobs);
-    hipLaunchKernelGGL(gemm_kernel, grid, dim3(NT), 0, stream, *p);
+    /* buffer offsets are 32-bit: each weight and its (s, b') table below 2 GB */
+    int64_t tiles = 0;
+    for (int j = 0; j < p->njobs; j++) {
+        const Q35Mlx4GemmJob *J = &p->jobs[j];
+        if (J->N < 1 || !J->vals || !J->sb || !J->y || J->ldy < J->N ||
+            (int64_t)J->N * p->K / 2 >= ((int64_t)1 << 31) ||
+            (int64_t)(p->K / 64) * q35_mlx4_sb_npad(J->N) * 8 >= ((int64_t)1 << 31))
+            return hipErrorInvalidValue;
+        tiles += (J->N + NTILE - 1) / NTILE;
+    }
+    tiles *= p->Mpad / MT;
+    if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm_kernel, dim3((unsigned)tiles), dim3(NT), 0, stream, *p);
     return hipGetLastError();
 }
 

@@ -111,6 +111,46 @@ __device__ __forceinline__ T q35_half_sum(T v) {
     return (threadIdx.x & 32) ? hi : lo;
 }
 
+/* Direct-to-LDS loads (buffer_load ... lds): lane l's 16 (dma16) or 4
+ * (dma4) bytes from buffer offset soff + voff, range-checked against the
+ * resource, land at LDS byte lds + 16 l (4 l).  Issued as inline assembly
+ * so the compiler's wait insertion does not see them: it cannot tell LDS
+ * stages apart and would wait for every staging load in flight before the
+ * next LDS read.  A kernel using them orders them itself (q35_wait_vm
+ * before the barrier that publishes a stage); loads the compiler does not
+ * count can only make its own load waits stricter. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   /* m0 is reserved; nothing else here uses it */
+__device__ __forceinline__ void q35_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff,
+                                          uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void q35_dma4(__amdgpu_buffer_rsrc_t rs, uint32_t lds, uint32_t voff,
+                                         uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rs), "s"(soff)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+/* s_waitcnt vmcnt(N), expcnt and lgkmcnt left open: at most N of this
+ * wave's vector memory loads (direct-to-LDS ones included) in flight */
+template <int N>
+__device__ __forceinline__ void q35_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+/* LDS byte address of a shared-memory pointer (for M0) */
+template <typename T>
+__device__ __forceinline__ uint32_t q35_lds_addr(T *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) T *)p;
+}
+
 /* Workgroup barrier that orders LDS only.  __syncthreads() carries a
  * workgroup-scope fence over all address spaces, which gfx950 implements as
  * s_waitcnt vmcnt(0) lgkmcnt(0) before s_barrier: every global load in

@@ -156,36 +156,39 @@ hipError_t q35_mlx4_matvec(const Q35Mlx4 *p, int njobs, hipStream_t stream);
 /* ---- MLX 4-bit projections of a prefill chunk on MFMA (mlx4_gemm.hip) ----
  * Y[M][N] = X[M][K] W^T for [N x K] 4-bit weights, K % 64 == 0.  X goes
  * through q35_mlx4_xprep first (optional RMSNorm, fp16 hi / lo in word
- * order, group sums); the weight's scales / biases through q35_mlx4_sb
- * once ((s, b - 1024 s) per row and group). */
+ * order, tiled per 64 rows and group; group sums); the weight's scales /
+ * biases through q35_mlx4_sb once ((16 s, b - 16 s) per group and row). */
 typedef struct Q35Mlx4Xprep {
     const float *x;                /* [M][ldx] */
     const uint16_t *norm_w;        /* [K] or NULL */
-    uint16_t *xh, *xl;             /* [Mpad][K] */
+    uint16_t *xw;                  /* Mpad * K * 2 halfs: hi / lo blocks per (64-row tile, group) */
     float *xsum;                   /* [K/64][Mpad] */
     int M, Mpad, K, ldx;
 } Q35Mlx4Xprep;
 typedef struct Q35Mlx4SB {
-    float s, b;                    /* scale, bias - 1024 * scale */
+    float s, b;                    /* 16 scale, bias - 16 scale */
 } Q35Mlx4SB;
 #define Q35_GEMM_MAX_JOBS 4
 typedef struct Q35Mlx4GemmJob {
     const uint32_t *vals;          /* [N][K/8] */
-    const Q35Mlx4SB *sb;           /* [N][K/64] */
-    int N;
+    const Q35Mlx4SB *sb;           /* [K/64][q35_mlx4_sb_npad(N)] */
+    float *y;                      /* [M][ldy] */
+    int N, ldy;
 } Q35Mlx4GemmJob;
+/* the jobs ride in the kernel arguments; one launch covers every job's
+ * 256-feature tiles */
 typedef struct Q35Mlx4Gemm {
-    const uint16_t *xh, *xl;
+    const uint16_t *xw;
     const float *xsum;
-    const Q35Mlx4GemmJob *jobs;    /* device array of njobs (static per weight set) */
-    float *y[Q35_GEMM_MAX_JOBS];   /* job j's output [M][ldy[j]] */
-    int ldy[Q35_GEMM_MAX_JOBS];
-    int M, Mpad, K, accumulate;    /* accumulate: y += instead of y = */
+    Q35Mlx4GemmJob jobs[Q35_GEMM_MAX_JOBS];
+    int njobs, M, Mpad, K, accumulate;   /* accumulate: y += instead of y = */
 } Q35Mlx4Gemm;
-hipError_t q35_mlx4_sb(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int64_t n,
+/* the (s, b') table of an N-row weight with G groups a row: G x npad(N) */
+int q35_mlx4_sb_npad(int N);
+hipError_t q35_mlx4_sb(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int N, int G,
                        hipStream_t stream);
 hipError_t q35_mlx4_xprep(const Q35Mlx4Xprep *p, hipStream_t stream);
-hipError_t q35_mlx4_gemm(const Q35Mlx4Gemm *p, int njobs, int max_n, hipStream_t stream);
+hipError_t q35_mlx4_gemm(const Q35Mlx4Gemm *p, hipStream_t stream);
 int q35_mlx4_gemm_mtile(void);      /* Mpad must be a multiple of this */
 
 #ifdef __cplusplus
