@@ -1030,7 +1030,7 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
         outw = &w->out;
     }
     Part pt[40];
-    const void *pv[5], *ps[5], *pb[5], *psb[5], *in_norm, *jobs, *t0, *t1, *t2, *t3;
+    const void *pv[5], *ps[5], *pb[5], *psb[5], *pwt[5], *in_norm, *jobs, *t0, *t1, *t2, *t3;
     int n = 0;
     for (int i = 0; i < np; i++) n += mlx4_parts(pt + n, proj[i], &pv[i], &ps[i], &pb[i]);
     n += mlx4_parts(pt + n, outw, &pv[4], &ps[4], &pb[4]);
@@ -1041,6 +1041,8 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
         pt[n++] = (Part){NULL,
                          m ? (size_t)q35_mlx4_sb_npad(m->rows) * (m->cols / 64) * sizeof(Q35Mlx4SB) : 0,
                          &psb[i]};
+        /* the words again, re-laid out for the GEMM's staging */
+        pt[n++] = (Part){NULL, m ? (size_t)q35_mlx4_sb_npad(m->rows) * m->cols / 2 : 0, &pwt[i]};
     }
     pt[n++] = (Part){w->in_norm, w->in_norm ? (size_t)hidden * 2 : 0, &in_norm};
     pt[n++] = (Part){NULL, (size_t)np * sizeof(Q35Mlx4Job), &jobs};   /* filled below */
@@ -1082,13 +1084,15 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
         if (!m) continue;
         if (q35_mlx4_sb((const uint16_t *)ps[i], (const uint16_t *)pb[i], (Q35Mlx4SB *)psb[i],
                         m->rows, m->cols / 64, P.stream) != hipSuccess ||
+            q35_mlx4_wt((const uint32_t *)pv[i], (uint32_t *)pwt[i], m->rows, m->cols, P.stream) !=
+                hipSuccess ||
             hipStreamSynchronize(P.stream) != hipSuccess) {
             set_err("layer weights: scale table failed");
             hipFree(lw->d);
             memset(lw, 0, sizeof *lw);
             return -1;
         }
-        lw->gj[ng++] = (Q35Mlx4GemmJob){(const uint32_t *)pv[i], (const Q35Mlx4SB *)psb[i], NULL,
+        lw->gj[ng++] = (Q35Mlx4GemmJob){(const uint32_t *)pwt[i], (const Q35Mlx4SB *)psb[i], NULL,
                                         m->rows, 0};
     }
     lw->in_norm = (const uint16_t *)in_norm;

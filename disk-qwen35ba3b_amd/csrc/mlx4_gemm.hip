@@ -31,7 +31,11 @@
  *   xsum    fp32 [G][Mpad];
  *   sb      (sb_kernel) (16 s, b - 16 s) as [G][Npad], Npad = N rounded up
  *           to 256, zeros past N;
- *   weights the MLX words as they are, [N][K/8].
+ *   wt      (wt_kernel) the weight words re-laid out once per weight: per
+ *           256-feature tile and group an 8 KB block that is the LDS image
+ *           of the stage (16-byte position p = row p / 2, half
+ *           wslot(row, p % 2)), rows past N zero; staging it is a plain
+ *           copy, 1 KB a wave load.
  * In a group (8 words), MFMA k-step ks of lane half h is word 4h + ks: a
  * lane's weight operand for a whole group is one 16-byte read.
  *
@@ -40,7 +44,8 @@
  * B = W^T converted in registers).  Every global load is a direct-to-LDS
  * load into a ring of three stages, one group each (X hi and lo 16 KB,
  * the tile's weight words 8 KB, (s, b') 2 KB, xsum 256 B), issued two
- * groups ahead; each wave waits for its own loads of the next group
+ * groups ahead (every stage load a contiguous 1 KB); each wave waits for
+ * its own loads of the next group
  * before the one barrier a group.  Two workgroups fit a CU (157.5 KB of
  * LDS), two waves a SIMD.
  */
@@ -157,6 +162,23 @@ __global__ void sb_kernel(const uint16_t *scales, const uint16_t *biases, Q35Mlx
     sb[i] = Q35Mlx4SB{sv, bv};
 }
 
+/* the weight words [N][K/8] as wt blocks [npad/256][G][512 granules of
+ * 16 bytes]: granule p of block (tile, g) = words 4 wslot(r, p % 2) ..
+ * +3 of group g of row tile * 256 + r, r = p / 2; zeros past N */
+__global__ void wt_kernel(const uint32_t *vals, u32x4_t *wt, int N, int K, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int G = K / 64;
+    const int p = (int)(i & 511);
+    const int64_t blk = i >> 9;
+    const int g = (int)(blk % G), tile = (int)(blk / G);
+    const int r = p >> 1, row = tile * NTILE + r;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (row < N)
+        v = *reinterpret_cast<const u32x4_t *>(vals + (size_t)row * (K / 8) + 8 * g + 4 * wslot(r, p & 1));
+    wt[i] = v;
+}
+
 /* a word's 8 nibbles as the fp16 B operand 1 + q / 16, in word order:
  * pair j (nibbles j and j + 4, bits 4j and 16 + 4j) shifted to bits 6 and
  * 22, masked, ORed into the exponent of 1.  The mask and the exponent bits
@@ -208,23 +230,12 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         q35_uniform_ptr(const_cast<uint16_t *>(p.xw)), 0, (int)((size_t)p.Mpad * p.K * 4), Q35_BUF_DW3);
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<uint32_t *>(J.vals)), 0, (int)((size_t)J.N * p.K / 2), Q35_BUF_DW3);
+        q35_uniform_ptr(const_cast<uint32_t *>(J.vals)), 0, (int)((size_t)npad * p.K / 2), Q35_BUF_DW3);
     const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
         q35_uniform_ptr(const_cast<Q35Mlx4SB *>(J.sb)), 0, (int)((size_t)G * npad * 8), Q35_BUF_DW3);
     const __amdgpu_buffer_rsrc_t ssr = __builtin_amdgcn_make_buffer_rsrc(
         q35_uniform_ptr(const_cast<float *>(p.xsum)), 0, (int)((size_t)G * p.Mpad * 4), Q35_BUF_DW3);
 
-    /* weight staging: load i (of 8, this wave's w and w + 4) puts 16-byte
-     * LDS position 64 i + lane, row r = position / 2 in slot position & 1,
-     * which holds half wslot(r, slot) of the row (wslot is its own inverse
-     * in h); rows past N read row N - 1, whose products no lane stores */
-    uint32_t wv[2];
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int pos = 64 * (w + 4 * q) + lane, r = pos >> 1;
-        const int n = n0 + r < J.N ? n0 + r : J.N - 1;
-        wv[q] = (uint32_t)n * (uint32_t)(p.K / 2) + (uint32_t)wslot(r, pos & 1) * 16;
-    }
     /* group g into stage st: X 16 loads, weights 8, (s, b') 2, xsum 1 (a
      * dword load); waves 0-2 issue 7 of them, wave 3 issues 6 */
     auto issue = [&](int g, int st) {
@@ -235,9 +246,12 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
             const int i = w + 4 * q;
             q35_dma16(xr, sb + i * 1024, lane * 16, xb + i * 1024);
         }
+        const uint32_t wb = (uint32_t)(nt * G + g) * WBLK;
 #pragma unroll
-        for (int q = 0; q < 2; q++)
-            q35_dma16(wr, sb + OFF_W + (w + 4 * q) * 1024, wv[q], (uint32_t)g * 32);
+        for (int q = 0; q < 2; q++) {
+            const int i = w + 4 * q;
+            q35_dma16(wr, sb + OFF_W + i * 1024, lane * 16, wb + i * 1024);
+        }
         if (w < 2)
             q35_dma16(sr, sb + OFF_SB + w * 1024, lane * 16, (uint32_t)(g * npad + n0) * 8 + w * 1024);
         else if (w == 2)
@@ -384,6 +398,14 @@ extern "C" hipError_t q35_mlx4_sb(const uint16_t *scales, const uint16_t *biases
 
 extern "C" int q35_mlx4_sb_npad(int N) { return (N + NTILE - 1) / NTILE * NTILE; }
 
+extern "C" hipError_t q35_mlx4_wt(const uint32_t *vals, uint32_t *wt, int N, int K, hipStream_t stream) {
+    if (N < 1 || K < 64 || K % 64 != 0) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)q35_mlx4_sb_npad(N) * (K / 64) * 2;   /* granules */
+    hipLaunchKernelGGL(wt_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, vals,
+                       reinterpret_cast<u32x4_t *>(wt), N, K, n);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t q35_mlx4_xprep(const Q35Mlx4Xprep *p, hipStream_t stream) {
     if (p->K % 64 != 0 || p->K > 8192 || p->Mpad % MT != 0 || p->M > p->Mpad || p->M < 1)
         return hipErrorInvalidValue;
@@ -401,7 +423,7 @@ extern "C" hipError_t q35_mlx4_gemm(const Q35Mlx4Gemm *p, hipStream_t stream) {
     for (int j = 0; j < p->njobs; j++) {
         const Q35Mlx4GemmJob *J = &p->jobs[j];
         if (J->N < 1 || !J->vals || !J->sb || !J->y || J->ldy < J->N ||
-            (int64_t)J->N * p->K / 2 >= ((int64_t)1 << 31) ||
+            (int64_t)q35_mlx4_sb_npad(J->N) * p->K / 2 >= ((int64_t)1 << 31) ||
             (int64_t)(p->K / 64) * q35_mlx4_sb_npad(J->N) * 8 >= ((int64_t)1 << 31))
             return hipErrorInvalidValue;
         tiles += (J->N + NTILE - 1) / NTILE;

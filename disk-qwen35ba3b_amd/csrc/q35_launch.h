@@ -170,7 +170,7 @@ typedef struct Q35Mlx4SB {
 } Q35Mlx4SB;
 #define Q35_GEMM_MAX_JOBS 4
 typedef struct Q35Mlx4GemmJob {
-    const uint32_t *vals;          /* [N][K/8] */
+    const uint32_t *vals;          /* the words re-laid out by q35_mlx4_wt */
     const Q35Mlx4SB *sb;           /* [K/64][q35_mlx4_sb_npad(N)] */
     float *y;                      /* [M][ldy] */
     int N, ldy;
@@ -187,6 +187,9 @@ typedef struct Q35Mlx4Gemm {
 int q35_mlx4_sb_npad(int N);
 hipError_t q35_mlx4_sb(const uint16_t *scales, const uint16_t *biases, Q35Mlx4SB *sb, int N, int G,
                        hipStream_t stream);
+/* the weight words [N][K/8] re-laid out for the GEMM's staging:
+ * npad(N) * K / 2 bytes */
+hipError_t q35_mlx4_wt(const uint32_t *vals, uint32_t *wt, int N, int K, hipStream_t stream);
 hipError_t q35_mlx4_xprep(const Q35Mlx4Xprep *p, hipStream_t stream);
 hipError_t q35_mlx4_gemm(const Q35Mlx4Gemm *p, hipStream_t stream);
 int q35_mlx4_gemm_mtile(void);      /* Mpad must be a multiple of this */
