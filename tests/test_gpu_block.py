@@ -17,6 +17,7 @@ import sys
 import numpy as np
 import pytest
 
+import f64_model as F
 import oracle as O
 from ds4f_hip import synth as SY
 from ds4f_hip import workloads as W
@@ -209,5 +210,45 @@ def test_chunk_matches_oracle(kind, t0, B):
             mx, rr = _err(st_g, st_o)
             _say(f"  decode after chunk, token {tok}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
+    finally:
+        ga.close()
+
+
+def test_gqa_chunk_4096_sampled():
+    """A 4096-token prefill chunk through a GQA layer from an empty cache
+    (the prefill workload's size), its rows at sampled tokens checked
+    against the oracle's layer step at that token over fp32 cache rows of
+    the tokens before it (their k / v projections in float64, then the
+    oracle's cache-row helper for norm and RoPE): each sampled row is the
+    same computation as the chunk's, without the oracle's 4096 serial
+    steps.  The device attends over fp16 copies of its fp32 k / v, so the
+    reference rows are fp32, not the bf16 rows the device stores: with few
+    keys (early tokens) the bf16 rounding of a row would reach the output
+    undamped (6e-3 at token 1)."""
+    T = 4096
+    ga, ref, ws = _stack([2], 0, 0, T + 64)
+    try:
+        _say(f"gqa chunk T={T}")
+        states = np.stack([W.hidden_state(HID, 0, 3000 + b) for b in range(T)])
+        got = ga.attn_chunk(0, 0, states)
+        assert np.isfinite(got).all()
+        w = ws[0]
+        xin = F.rmsnorm(states, F.bf(w.in_norm))
+        kp = (xin @ F.mlx4_dense(w.k).T).astype(np.float32)
+        vp = (xin @ F.mlx4_dense(w.v).T).astype(np.float32)
+        rows = np.zeros((T + 64, 2 * GQ.kv_heads * GQ.head_dim), np.float32)
+        rows[:T] = O.gqa_cache_rows(kp, vp, w.kn, 0, GQ.kv_heads, GQ.head_dim)
+        rng = np.random.default_rng(11)
+        samples = sorted(set([0, 1, 15, 16, 17, 63, 64, 1000, 2047, 4095] +
+                             [int(x) for x in rng.integers(0, T, 6)]))
+        worst = 0.0
+        for t in samples:
+            kv = rows.copy()
+            exp = O.gqa_step(kv, t, states[t], ws[0], GQ.heads, GQ.kv_heads, GQ.head_dim)
+            e = _err(got[t], exp)
+            _say(f"  token {t}: max scaled err {e[0]:.3e} rel-rms {e[1]:.3e}")
+            worst = max(worst, e[0])
+        _say(f"  sampled tokens {len(samples)}: worst max scaled err {worst:.3e}")
+        assert worst <= ATOL
     finally:
         ga.close()
