@@ -252,3 +252,32 @@ def test_gqa_chunk_4096_sampled():
         assert worst <= ATOL
     finally:
         ga.close()
+
+
+@pytest.mark.parametrize("kind", [2, 1])
+def test_chunk_past_the_cache_end(kind):
+    """A chunk running past max_tokens updates the rows of the tokens that
+    fit and leaves the rest untouched, as the oracle's chunk (serial layer
+    steps, each a silent skip past max_tokens: src/attn_qwen.c:117, :882);
+    a chunk starting at max_tokens changes nothing."""
+    mt = 64
+    t0 = mt - 3
+    ga, ref, ws = _stack([kind], t0, t0, mt)
+    try:
+        states = np.stack([W.hidden_state(HID, 0, 800 + b) for b in range(5)])
+        got = ga.attn_chunk(0, t0, states)
+        if kind == 2:
+            exp = O.gqa_chunk(ref[0], t0, states, ws[0], GQ.heads, GQ.kv_heads, GQ.head_dim)
+        else:
+            ring, S = ref[0]
+            exp = O.lin_chunk(ring, S, t0, states, ws[0], LG.k_heads, LG.v_heads, LG.kd, LG.vd,
+                              max_tokens=mt)
+        mx, rr = _err(got, exp)
+        _say(f"chunk kind {kind} t0 {t0} B 5 max_tokens {mt}: max scaled err {mx:.3e}")
+        assert mx <= ATOL
+        assert np.array_equal(got[3:], states[3:]) and np.array_equal(exp[3:], states[3:])
+        assert not np.array_equal(got[:3], states[:3])
+        again = ga.attn_chunk(0, mt, states)
+        assert np.array_equal(again, states)
+    finally:
+        ga.close()
