@@ -291,68 +291,67 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
     int st = 0;
     for (int g = 0; g < G; g++) {
         if (g + 2 < G) issue(g + 2, st == 0 ? 2 : st - 1);
-        if (idle) goto next;
-        {
-        const uint8_t *S = smem + st * STAGE;
-        /* the weight operand: this lane's words 4h..4h+3 of rows
-         * 64w + 32nb + c, and their (s, b') */
-        f16x8_t bf[2][4];
-        float sc[2], bp[2];
+        if (!idle) {
+            const uint8_t *S = smem + st * STAGE;
+            /* the weight operand: this lane's words 4h..4h+3 of rows
+             * 64w + 32nb + c, and their (s, b') */
+            f16x8_t bf[2][4];
+            float sc[2], bp[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; nb++) {
-            const int r = 64 * w + 32 * nb + c;
-            const u32x4_t wq = *reinterpret_cast<const u32x4_t *>(S + OFF_W + r * 32 + wslot(r, h) * 16);
+            for (int nb = 0; nb < 2; nb++) {
+                const int r = 64 * w + 32 * nb + c;
+                const u32x4_t wq = *reinterpret_cast<const u32x4_t *>(S + OFF_W + r * 32 + wslot(r, h) * 16);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) bf[nb][ks] = nib_f16(wq[ks], mask, one);
-            const float2 v = *reinterpret_cast<const float2 *>(S + OFF_SB + r * 8);
-            sc[nb] = v.x;
-            bp[nb] = v.y;
-        }
+                for (int ks = 0; ks < 4; ks++) bf[nb][ks] = nib_f16(wq[ks], mask, one);
+                const float2 v = *reinterpret_cast<const float2 *>(S + OFF_SB + r * 8);
+                sc[nb] = v.x;
+                bp[nb] = v.y;
+            }
 
-        f32x16_t tmp[2][2];
+            f32x16_t tmp[2][2];
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            f16x8_t ah[2], al[2];
+            for (int ks = 0; ks < 4; ks++) {
+                f16x8_t ah[2], al[2];
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++) {
+                    const int r = 32 * mb + c;
+                    const int off = r * 128 + xslot(r, 4 * h + ks) * 16;
+                    ah[mb] = *reinterpret_cast<const f16x8_t *>(S + off);
+                    al[mb] = *reinterpret_cast<const f16x8_t *>(S + XBLK + off);
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                    for (int nb = 0; nb < 2; nb++) {
+                        if (ks == 0) {
+                            f32x16_t z;
+#pragma unroll
+                            for (int i = 0; i < 16; i++) z[i] = 0.0f;
+                            tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mb], bf[nb][ks], z, 0, 0, 0);
+                        } else {
+                            tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mb], bf[nb][ks],
+                                                                                 tmp[mb][nb], 0, 0, 0);
+                        }
+                        tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[mb], bf[nb][ks], tmp[mb][nb], 0, 0, 0);
+                    }
+            }
+            /* acc += s * partial + b' * xsum; lane rows 32mb + 8(i/4) + 4h + i%4 */
+            const float *xs = reinterpret_cast<const float *>(S + OFF_XS);
 #pragma unroll
             for (int mb = 0; mb < 2; mb++) {
-                const int r = 32 * mb + c;
-                const int off = r * 128 + xslot(r, 4 * h + ks) * 16;
-                ah[mb] = *reinterpret_cast<const f16x8_t *>(S + off);
-                al[mb] = *reinterpret_cast<const f16x8_t *>(S + XBLK + off);
-            }
+                float xsv[16];
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++) {
-                    if (ks == 0) {
-                        f32x16_t z;
-#pragma unroll
-                        for (int i = 0; i < 16; i++) z[i] = 0.0f;
-                        tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mb], bf[nb][ks], z, 0, 0, 0);
-                    } else {
-                        tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[mb], bf[nb][ks], tmp[mb][nb], 0, 0, 0);
-                    }
-                    tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[mb], bf[nb][ks], tmp[mb][nb], 0, 0, 0);
+                for (int q = 0; q < 4; q++) {
+                    const float4 v = *reinterpret_cast<const float4 *>(xs + 32 * mb + 8 * q + 4 * h);
+                    xsv[4 * q] = v.x, xsv[4 * q + 1] = v.y, xsv[4 * q + 2] = v.z, xsv[4 * q + 3] = v.w;
                 }
-        }
-        /* acc += s * partial + b' * xsum; lane rows 32mb + 8(i/4) + 4h + i%4 */
-        const float *xs = reinterpret_cast<const float *>(S + OFF_XS);
 #pragma unroll
-        for (int mb = 0; mb < 2; mb++) {
-            float xsv[16];
+                for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 v = *reinterpret_cast<const float4 *>(xs + 32 * mb + 8 * q + 4 * h);
-                xsv[4 * q] = v.x, xsv[4 * q + 1] = v.y, xsv[4 * q + 2] = v.z, xsv[4 * q + 3] = v.w;
+                    for (int i = 0; i < 16; i++)
+                        acc[mb][nb][i] = fmaf(sc[nb], tmp[mb][nb][i], fmaf(bp[nb], xsv[i], acc[mb][nb][i]));
             }
-#pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    acc[mb][nb][i] = fmaf(sc[nb], tmp[mb][nb][i], fmaf(bp[nb], xsv[i], acc[mb][nb][i]));
         }
-        }
-    next:
         /* the next group's stage is complete for every wave; this one is
          * free for the load issued next iteration */
         if (g + 2 < G)
