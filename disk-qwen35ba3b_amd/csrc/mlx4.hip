@@ -8,7 +8,7 @@
  * of the flattened matrix is nibble k%8 of word k/8; a BF16 scale and bias
  * per 64 elements (group k/64, which may straddle rows); w = q*scale+bias.
  *
- * One wave per 8 / NCH rows (NCH = 2048-column chunks of x), their loads
+ * One wave per 4 / NCH rows (NCH = 2048-column chunks of x; 1 at 8192), their loads
  * and the next rows' issued together; lane l takes 32 consecutive elements
  * (one 16-byte word load) of each 2048-column chunk.
  * With C % 32 == 0 those 32 elements start 32-aligned in the flattened
@@ -70,9 +70,13 @@ __device__ __forceinline__ float nib_dot(u32x4_t w, const float (&x)[32]) {
     return a0 + a1;
 }
 
-/* rows a wave takes per iteration: 8 2048-column chunks' worth of loads */
+/* rows a wave takes per iteration: 4 2048-column chunks' worth of loads
+ * (one row at 8192 columns).  Measured against 8 and 2 on the 40-layer
+ * step and the 248320-row head: 4 is faster on both (a layer's 12352
+ * projection rows then give 3088 waves, 3 workgroups a CU, instead of
+ * 1.5) */
 template <int NCH>
-constexpr int rows_per_wave() { return 8 / NCH; }
+constexpr int rows_per_wave() { return NCH >= 4 ? 1 : 4 / NCH; }
 
 template <int NCH, bool NORM>
 __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
