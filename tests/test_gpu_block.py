@@ -281,3 +281,28 @@ def test_chunk_past_the_cache_end(kind):
         assert np.array_equal(again, states)
     finally:
         ga.close()
+
+
+@pytest.mark.parametrize("kind", [2, 1])
+def test_consecutive_chunks_grow_the_workspace(kind):
+    """Chunks of 20, 100 and 7 tokens in a row on one binding (the
+    workspaces grow on the second), each continuing the cache / state the
+    previous one left, against the oracle's chunks in the same order."""
+    t = 5
+    ga, ref, ws = _stack([kind], t, t, 256)
+    try:
+        for n, B in enumerate((20, 100, 7)):
+            states = np.stack([W.hidden_state(HID, 0, 1200 + 200 * n + b) for b in range(B)])
+            got = ga.attn_chunk(0, t, states)
+            if kind == 2:
+                exp = O.gqa_chunk(ref[0], t, states, ws[0], GQ.heads, GQ.kv_heads, GQ.head_dim)
+                ref[0][t:t + B] = SY.bf16_round(ref[0][t:t + B])   # the device's stored rows
+            else:
+                ring, S = ref[0]
+                exp = O.lin_chunk(ring, S, t, states, ws[0], LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+            mx, rr = _err(got, exp)
+            _say(f"chunk kind {kind} t0 {t} B {B}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+            t += B
+    finally:
+        ga.close()
