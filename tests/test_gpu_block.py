@@ -306,3 +306,27 @@ def test_consecutive_chunks_grow_the_workspace(kind):
             t += B
     finally:
         ga.close()
+
+
+def test_four_layer_stack_one_chunk():
+    """A lin-lin-lin-GQA stack (the model's layer pattern) over one chunk of
+    40 tokens at t0 = 9, each layer's chunk taking the states the previous
+    layer's chunk left, against the oracle's chunks chained the same way."""
+    kinds = [1, 1, 1, 2]
+    t0, B = 9, 40
+    ga, ref, ws = _stack(kinds, t0, t0, 256, seed=3)
+    try:
+        st_g = np.stack([W.hidden_state(HID, 3, 1500 + b) for b in range(B)])
+        st_o = st_g.copy()
+        for L, kind in enumerate(kinds):
+            st_g = ga.attn_chunk(L, t0, st_g)
+            if kind == 2:
+                st_o = O.gqa_chunk(ref[L], t0, st_o, ws[L], GQ.heads, GQ.kv_heads, GQ.head_dim)
+            else:
+                ring, S = ref[L]
+                st_o = O.lin_chunk(ring, S, t0, st_o, ws[L], LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+            mx, rr = _err(st_g, st_o)
+            _say(f"stack chunk layer {L} kind {kind}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+    finally:
+        ga.close()
