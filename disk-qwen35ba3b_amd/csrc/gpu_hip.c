@@ -471,11 +471,13 @@ int ds4f_hip_lin_decode_async(int L, int token, const float *qkv, const float *z
     return 0;
 }
 
-int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const float *z,
-                               const float *a, const float *b, const uint16_t *conv_w,
-                               const float *A_log, const uint16_t *dt_bias,
-                               const uint16_t *norm_w, float *out, float *qkv_post,
-                               void *stream) {
+/* the delta-rule prefill; xw non-NULL: the gated norm writes the chunk
+ * GEMM's X operand (xw, xsum over mpad rows) instead of out */
+static int lin_prefill_launch(int L, int t0, int B, const float *qkv, const float *z,
+                              const float *a, const float *b, const uint16_t *conv_w,
+                              const float *A_log, const uint16_t *dt_bias, const uint16_t *norm_w,
+                              float *out, float *qkv_post, uint16_t *xw, float *xsum, int mpad,
+                              void *stream) {
     if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
     if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;   /* src/attn_qwen.c:882 */
     if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
@@ -517,8 +519,20 @@ int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const flo
     CARVE(p.Pm, nc * vh * 64 * 64);
     CARVE(p.gvec, nc * vh * Q35_LIN_GVEC);
 #undef CARVE
+    p.xw = xw;
+    p.xsum = xsum;
+    p.mpad = mpad;
     HIPCHK(q35_lin_prefill(&p, pick(stream)));
     return 0;
+}
+
+int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const float *z,
+                               const float *a, const float *b, const uint16_t *conv_w,
+                               const float *A_log, const uint16_t *dt_bias,
+                               const uint16_t *norm_w, float *out, float *qkv_post,
+                               void *stream) {
+    return lin_prefill_launch(L, t0, B, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, out, qkv_post,
+                              NULL, NULL, 0, stream);
 }
 
 /* ---- host-pointer entry points ----------------------------------------- */
@@ -1247,13 +1261,15 @@ static int ensure_chunk(int B, ChunkWs *ws) {
     return 0;
 }
 
-/* X = [norm](x rows), then y = X W^T for the njobs GEMM jobs, job j
- * writing ys[j] [B][lds[j]] */
+/* X = [norm](x rows) (x NULL: the workspace already holds X), then
+ * y = X W^T for the njobs GEMM jobs, job j writing ys[j] [B][lds[j]] */
 static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, int B,
                       const Q35Mlx4GemmJob *jobs, int njobs, float *const *ys, const int *lds,
                       int accumulate, const ChunkWs *ws, hipStream_t st) {
-    Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, P.chunk_cap, K, ldx};
-    HIPCHK(q35_mlx4_xprep(&xp, st));
+    if (x) {
+        Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, P.chunk_cap, K, ldx};
+        HIPCHK(q35_mlx4_xprep(&xp, st));
+    }
     Q35Mlx4Gemm g;
     memset(&g, 0, sizeof g);
     g.xw = ws->xw;
@@ -1314,17 +1330,19 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
             return -1;
         core_out = CH_AO;
     } else {
-        if (ds4f_hip_lin_prefill_async(L, t0, B, ws.out[CH_QKV], ws.out[CH_Z], ws.out[CH_A],
-                                       ws.out[CH_B], lw->conv_w, lw->A_log, lw->dt_bias,
-                                       lw->norm_w, ws.out[CH_LO], NULL, st) != 0)
+        /* the gated norm writes the output GEMM's X operand directly */
+        if (lin_prefill_launch(L, t0, B, ws.out[CH_QKV], ws.out[CH_Z], ws.out[CH_A], ws.out[CH_B],
+                               lw->conv_w, lw->A_log, lw->dt_bias, lw->norm_w, ws.out[CH_LO], NULL,
+                               ws.xw, ws.xsum, P.chunk_cap, st) != 0)
             return -1;
-        core_out = CH_LO;
+        core_out = -1;
     }
     /* the output projection, added to the rows' states */
     float *yo[1] = {states};
     const int ldo[1] = {H};
-    return chunk_gemm(ws.out[core_out], (int)ch_width(core_out), NULL, (int)ch_width(core_out), B,
-                      lw->gj + lw->njobs, 1, yo, ldo, 1, &ws, st);
+    const int K = (int)ch_width(kind == DS4F_LAYER_GQA ? CH_AO : CH_LO);
+    return chunk_gemm(core_out >= 0 ? ws.out[core_out] : NULL, K, NULL, K, B, lw->gj + lw->njobs, 1,
+                      yo, ldo, 1, &ws, st);
 }
 
 int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {

@@ -639,6 +639,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 
 /* ---- 5. RMSNormGated per (token, value head), in place on out ----------- *
  * grid (VH / 4, B), wave w -> head 4*blockIdx.x + w, 2 columns a lane. */
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+
 __global__ __launch_bounds__(256) void gnorm_kernel(Q35LinPrefill p) {
     const int b = blockIdx.y;
     const int h = 4 * blockIdx.x + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -655,7 +657,34 @@ __global__ __launch_bounds__(256) void gnorm_kernel(Q35LinPrefill p) {
         y.x = o.x / r * q35_bf2f((uint16_t)(nw & 0xffff)) * (z.x * q35_sigmoid(z.x));
         y.y = o.y / r * q35_bf2f((uint16_t)(nw >> 16)) * (z.y * q35_sigmoid(z.y));
     }
-    *reinterpret_cast<float2 *>(p.out + off) = y;
+    if (!p.xw) {
+        *reinterpret_cast<float2 *>(p.out + off) = y;
+        return;
+    }
+    /* The chunk GEMM's X operand instead: quad lanes 4k..4k+3 hold word k
+     * of the head's 16 (values 2i, 2i + 1 in quad lane i); every lane of the
+     * quad gathers the word, lane 0 stores its hi granule, lane 1 its lo.
+     * The group sums (64 columns = one half wave) add the same hi + lo. */
+    float w8[8];
+    w8[0] = q35_dpp<0x00>(y.x), w8[1] = q35_dpp<0x00>(y.y);
+    w8[2] = q35_dpp<0x55>(y.x), w8[3] = q35_dpp<0x55>(y.y);
+    w8[4] = q35_dpp<0xAA>(y.x), w8[5] = q35_dpp<0xAA>(y.y);
+    w8[6] = q35_dpp<0xFF>(y.x), w8[7] = q35_dpp<0xFF>(y.y);
+    f16x8 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float v = w8[q35_xw_perm(j)];
+        hi[j] = (_Float16)v;
+        lo[j] = (_Float16)(v - (float)hi[j]);
+    }
+    const _Float16 hx = (_Float16)y.x, hy = (_Float16)y.y;
+    float s = ((float)hx + (float)(_Float16)(y.x - (float)hx)) + ((float)hy + (float)(_Float16)(y.y - (float)hy));
+    s = q35_half_sum(s);
+    const int G = p.v_heads * VD / 64, v = h * (VD / 8) + (lane >> 2);
+    uint8_t *gr = reinterpret_cast<uint8_t *>(p.xw) + q35_xw_granule(b, v, G);
+    if ((lane & 3) == 0) *reinterpret_cast<f16x8 *>(gr) = hi;
+    if ((lane & 3) == 1) *reinterpret_cast<f16x8 *>(gr + Q35_XW_BLK) = lo;
+    if ((lane & 31) == 0) p.xsum[(size_t)(v >> 3) * p.mpad + b] = s;
 }
 
 
@@ -686,6 +715,7 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(SCAN_THREADS), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (p.xw && (p.mpad < p.B || p.mpad % Q35_XW_ROWS != 0 || !p.xsum)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(gnorm_kernel, dim3(p.v_heads / 4, p.B), dim3(256), 0, stream, p);
     return hipGetLastError();
 }

@@ -59,7 +59,8 @@ namespace {
 constexpr int NT = 256;
 constexpr int MT = 64;                 /* tokens a tile */
 constexpr int NTILE = 256;             /* features a tile, 64 a wave */
-constexpr int XBLK = MT * 128;         /* bytes of a tile's hi (or lo) X of one group */
+constexpr int XBLK = Q35_XW_BLK;       /* bytes of a tile's hi (or lo) X of one group */
+static_assert(MT == Q35_XW_ROWS, "the X tiles are the GEMM's token tiles");
 constexpr int WBLK = NTILE * 32;       /* bytes of a tile's weight words of one group */
 constexpr int SBLK = NTILE * 8;        /* bytes of a tile's (s, b') of one group */
 constexpr int OFF_W = 2 * XBLK, OFF_SB = OFF_W + WBLK, OFF_XS = OFF_SB + SBLK;
@@ -67,14 +68,10 @@ constexpr int STAGE = OFF_XS + MT * 4; /* 26880 bytes */
 constexpr int NSTAGE = 3;
 constexpr float QSTEP = 16.0f;         /* B = 1 + q / QSTEP */
 
-/* the word's order of k inside a group: slot j of word v holds k = 8v + PERM[j] */
-__device__ __forceinline__ int perm8(int j) { return (j >> 1) + 4 * (j & 1); }
-
-/* 16-byte slot of word j of tile row r in its 128-byte X row; distinct
- * over any 8 consecutive rows and, with the row's 128-byte half, over any
- * 16: the operand reads are free of bank conflicts whether the LDS serves
- * 8 lanes over 32 banks or 16 lanes over 64 banks a cycle */
-__device__ __forceinline__ int xslot(int r, int j) { return j ^ (r & 7) ^ ((r >> 3) & 1); }
+/* q35_xw_slot: the 16-byte slot of word j of tile row r in its 128-byte X
+ * row is distinct over any 8 consecutive rows and, with the row's 128-byte
+ * half, over any 16: the operand reads are free of bank conflicts whether
+ * the LDS serves 8 lanes over 32 banks or 16 lanes over 64 banks a cycle */
 /* slot of half h (words 4h..4h+3) of tile feature row r in its 32-byte
  * weight row, by the same argument over 4 and 8 consecutive rows */
 __device__ __forceinline__ int wslot(int r, int h) { return h ^ (((r >> 2) ^ (r >> 3)) & 1); }
@@ -125,17 +122,14 @@ __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float v8 = e[perm8(j)];
+            const float v8 = e[q35_xw_perm(j)];
             const _Float16 h = (_Float16)v8;
             const _Float16 l = (_Float16)(v8 - (float)h);
             hi[j] = h;
             lo[j] = l;
             s += (float)h + (float)l;
         }
-        const int r = m & (MT - 1);
-        uint8_t *blk = reinterpret_cast<uint8_t *>(p.xw) +
-                       ((size_t)(m / MT) * (p.K / 64) + (v >> 3)) * 2 * XBLK + r * 128 +
-                       xslot(r, v & 7) * 16;
+        uint8_t *blk = reinterpret_cast<uint8_t *>(p.xw) + q35_xw_granule(m, v, p.K / 64);
         *reinterpret_cast<f16x8_t *>(blk) = hi;
         *reinterpret_cast<f16x8_t *>(blk + XBLK) = lo;
         /* the group's 8 words are 8 consecutive threads of a wave */
@@ -315,7 +309,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
 #pragma unroll
                 for (int mb = 0; mb < 2; mb++) {
                     const int r = 32 * mb + c;
-                    const int off = r * 128 + xslot(r, 4 * h + ks) * 16;
+                    const int off = r * 128 + q35_xw_slot(r, 4 * h + ks) * 16;
                     ah[mb] = *reinterpret_cast<const f16x8_t *>(S + off);
                     al[mb] = *reinterpret_cast<const f16x8_t *>(S + XBLK + off);
                 }

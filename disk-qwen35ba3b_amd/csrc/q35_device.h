@@ -111,6 +111,23 @@ __device__ __forceinline__ T q35_half_sum(T v) {
     return (threadIdx.x & 32) ? hi : lo;
 }
 
+/* The chunk GEMM's tiled X operand (written by its X prep and by the
+ * delta-rule prefill's gated norm): x[m][k] of rows K wide as fp16 hi and
+ * lo (x - hi), per 64-row tile and 64-column group g (G = K / 64) a 16 KB
+ * block, hi then lo, each 64 rows of 128 bytes.  Word v = k / 8 of tile
+ * row r sits at 16-byte slot (v % 8) ^ (r & 7) ^ ((r >> 3) & 1); half j of
+ * the granule holds k % 8 = q35_xw_perm(j), the order 0,4,1,5,2,6,3,7 in
+ * which a nibble word's values become fp16 pairs. */
+constexpr int Q35_XW_ROWS = 64;
+constexpr int Q35_XW_BLK = Q35_XW_ROWS * 128;
+__device__ __forceinline__ int q35_xw_slot(int r, int j) { return j ^ (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int q35_xw_perm(int j) { return (j >> 1) + 4 * (j & 1); }
+/* byte offset of the hi granule of word v of row m (lo: + Q35_XW_BLK) */
+__device__ __forceinline__ size_t q35_xw_granule(int m, int v, int G) {
+    const int r = m & (Q35_XW_ROWS - 1);
+    return ((size_t)(m / Q35_XW_ROWS) * G + (v >> 3)) * (2 * Q35_XW_BLK) + r * 128 + q35_xw_slot(r, v & 7) * 16;
+}
+
 /* Direct-to-LDS loads (buffer_load ... lds): lane l's 16 (dma16) or 4
  * (dma4) bytes from buffer offset soff + voff, range-checked against the
  * resource, land at LDS byte lds + 16 l (4 l).  Issued as inline assembly

@@ -55,6 +55,12 @@ typedef struct Q35LinPrefill {
     float *out;                    /* [B][VH*VD] */
     float *post, *gates, *T, *Pm, *gvec;
     int t0, B, n_chunks, k_heads, v_heads;
+    /* xw non-NULL: the gated norm writes its rows as the chunk GEMM's X
+     * operand (xw, xsum over mpad rows, mlx4_gemm.hip) instead of into out,
+     * which then only carries the scan's rows */
+    uint16_t *xw;
+    float *xsum;
+    int mpad;
 } Q35LinPrefill;
 /* workspace bytes, post included when with_post != 0 */
 void q35_lin_prefill_ws_bytes(int B, int k_heads, int v_heads, int with_post, size_t *bytes);
