@@ -302,6 +302,28 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
                 bp[nb] = v.y;
             }
 
+            /* acc += b' * xsum first: it does not wait for the MFMAs, so it
+             * runs while the previous wave's MFMAs hold the pipe */
+            {
+                const float *xs0 = reinterpret_cast<const float *>(S + OFF_XS);
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++) {
+                    float xsv[16];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v = *reinterpret_cast<const float4 *>(xs0 + 32 * mb + 8 * q + 4 * h);
+                        xsv[4 * q] = v.x, xsv[4 * q + 1] = v.y, xsv[4 * q + 2] = v.z, xsv[4 * q + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++) acc[mb][nb][i] = fmaf(bp[nb], xsv[i], acc[mb][nb][i]);
+                }
+            }
+            /* the group's MFMAs at raised wave priority, so that the SIMD's
+             * other wave does its VALU work around them rather than
+             * competing for the issue slot (output GEMM 126 -> 116 us) */
+            __builtin_amdgcn_s_setprio(1);
             f32x16_t tmp[2][2];
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
@@ -329,22 +351,14 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(Q35Mlx4Gemm p) {
                         tmp[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[mb], bf[nb][ks], tmp[mb][nb], 0, 0, 0);
                     }
             }
-            /* acc += s * partial + b' * xsum; lane rows 32mb + 8(i/4) + 4h + i%4 */
-            const float *xs = reinterpret_cast<const float *>(S + OFF_XS);
+            __builtin_amdgcn_s_setprio(0);
+            /* acc += s' * partial; lane rows 32mb + 8(i/4) + 4h + i%4 */
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++) {
-                float xsv[16];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 v = *reinterpret_cast<const float4 *>(xs + 32 * mb + 8 * q + 4 * h);
-                    xsv[4 * q] = v.x, xsv[4 * q + 1] = v.y, xsv[4 * q + 2] = v.z, xsv[4 * q + 3] = v.w;
-                }
+            for (int mb = 0; mb < 2; mb++)
 #pragma unroll
                 for (int nb = 0; nb < 2; nb++)
 #pragma unroll
-                    for (int i = 0; i < 16; i++)
-                        acc[mb][nb][i] = fmaf(sc[nb], tmp[mb][nb][i], fmaf(bp[nb], xsv[i], acc[mb][nb][i]));
-            }
+                    for (int i = 0; i < 16; i++) acc[mb][nb][i] = fmaf(sc[nb], tmp[mb][nb][i], acc[mb][nb][i]);
         }
         /* the next group's stage is complete for every wave; this one is
          * free for the load issued next iteration */
