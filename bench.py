@@ -83,6 +83,25 @@ def gqa_layer_bytes(n_past: int) -> int:
 LIN_LAYER_BYTES = 4448960   # state r+w 4 MiB, conv rows/weights, qkv, z, gates, output
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: logical CPUs (os.cpu_count and the
+    process's affinity set) and the CPU model from /proc/cpuinfo."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = None
+    return {"nproc": os.cpu_count(), "affinity_cpus": aff, "cpu_model": model}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,107 +145,23 @@ def main() -> int:
 
 
 def run_stack_decode(args) -> int:
-    import numpy as np
     import torch
 
-    from ds4f_hip import lib as L
-    from ds4f_hip import synth as S
-    from ds4f_hip import workloads as W
-    from ds4f_hip.attn import GpuAttention, KvCache, dptr
+    from ds4f_hip.stack import StackDecode
 
-    lib = L.load()
-    torch.cuda.init()
-    dev = torch.device("cuda:0")
-    gq, lg = W.GqaGeom(), W.LinGeom()
-    kinds = W.stack_kinds(40)
     N, K, WU, seed = args.ctx, args.steps, args.warmup, args.seed
     T = WU + K
-    max_tokens = N + T + 64
     want_cpu = not args.no_cpu_baseline
 
-    # ---- device state: bind (host arrays only when the CPU baseline needs them)
-    cache = KvCache(40, max_tokens) if want_cpu else None
-    ga = GpuAttention(kinds, max_tokens, cache)
-    for Lr, kd in enumerate(kinds):
-        if kd == 2:
-            L.check(lib.ds4f_hip_synth_gqa_cache(Lr, N, seed, S.tid(S.GQA_KCACHE, Lr),
-                                                 S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
-        else:
-            L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr), None),
-                    "synth state")
-            L.check(lib.ds4f_hip_synth_conv_history(Lr, N, seed, S.tid(S.LIN_CONVSTATE, Lr),
-                                                    None), "synth conv")
-
-    def synth(n, dtype, dist, p0, p1, tid, t=None):
-        if t is None:
-            t = torch.empty(n, dtype=torch.float32 if dtype == 0 else torch.int16, device=dev)
-        L.check(lib.ds4f_hip_synth(dptr(t), n, dtype, dist, p0, p1, seed, tid, None), "synth")
-        return t
-
-    # weights and per-(layer, step) activations, resident in HBM
-    layers = []
-    for Lr, kd in enumerate(kinds):
-        d = {"kind": kd}
-        if kd == 2:
-            d["qn"] = synth(gq.head_dim, 1, 0, 1.0, 0.1, S.tid(S.GQA_QNW, Lr))
-            d["kn"] = synth(gq.head_dim, 1, 0, 1.0, 0.1, S.tid(S.GQA_KNW, Lr))
-            nq, nk = gq.heads * 2 * gq.head_dim, gq.kv_heads * gq.head_dim
-            d["q"] = torch.empty((T, nq), dtype=torch.float32, device=dev)
-            d["k"] = torch.empty((T, nk), dtype=torch.float32, device=dev)
-            d["v"] = torch.empty((T, nk), dtype=torch.float32, device=dev)
-            for s in range(T):
-                pos = N + s
-                synth(nq, 0, 0, 0.0, 1.0, S.tid(S.GQA_QGATE, Lr, pos), d["q"][s])
-                synth(nk, 0, 0, 0.0, 1.0, S.tid(S.GQA_K, Lr, pos), d["k"][s])
-                synth(nk, 0, 0, 0.0, 1.0, S.tid(S.GQA_V, Lr, pos), d["v"][s])
-            d["out"] = torch.empty(gq.heads * gq.head_dim, dtype=torch.float32, device=dev)
-        else:
-            d["cw"] = synth(lg.rows * 4, 1, 0, 0.0, 0.1, S.tid(S.LIN_CONVW, Lr))
-            d["al"] = synth(lg.v_heads, 0, 1, 0.0, 2.7, S.tid(S.LIN_ALOG, Lr))
-            d["dt"] = synth(lg.v_heads, 1, 0, 0.0, 0.1, S.tid(S.LIN_DTB, Lr))
-            d["nw"] = synth(lg.vd, 1, 0, 1.0, 0.1, S.tid(S.LIN_NORMW, Lr))
-            nz = lg.v_heads * lg.vd
-            d["qkv"] = torch.empty((T, lg.rows), dtype=torch.float32, device=dev)
-            d["z"] = torch.empty((T, nz), dtype=torch.float32, device=dev)
-            d["a"] = torch.empty((T, lg.v_heads), dtype=torch.float32, device=dev)
-            d["b"] = torch.empty((T, lg.v_heads), dtype=torch.float32, device=dev)
-            for s in range(T):
-                st = s        # step index of the delta-rule activation streams
-                synth(lg.rows, 0, 0, 0.0, 1.0, S.tid(S.LIN_QKV, Lr, st), d["qkv"][s])
-                synth(nz, 0, 0, 0.0, 1.0, S.tid(S.LIN_Z, Lr, st), d["z"][s])
-                synth(lg.v_heads, 0, 0, 0.0, 1.0, S.tid(S.LIN_A, Lr, st), d["a"][s])
-                synth(lg.v_heads, 0, 0, 0.0, 1.0, S.tid(S.LIN_B, Lr, st), d["b"][s])
-            d["out"] = torch.empty(nz, dtype=torch.float32, device=dev)
-        layers.append(d)
-    torch.cuda.synchronize()
+    # device state and per-(layer, step) activations, resident in HBM; the
+    # host arrays are bound only when the CPU baseline needs the state
+    sd = StackDecode(N, T, seed, host_cache=want_cpu)
+    lib, ga, cache, layers, kinds = sd.lib, sd.ga, sd.cache, sd.layers, sd.kinds
+    gq, lg = sd.gq, sd.lg
     if want_cpu:
         ga.sync(-1, to_host=True, n_kv_tokens=N)       # initial state for the CPU sample
 
-    def launch_step(s, stream):
-        pos = N + s
-        for Lr, d in enumerate(layers):
-            if d["kind"] == 2:
-                rc = lib.ds4f_hip_gqa_decode_async(Lr, pos, dptr(d["q"][s]), dptr(d["k"][s]),
-                                                   dptr(d["v"][s]), dptr(d["qn"]), dptr(d["kn"]),
-                                                   dptr(d["out"]), None, stream)
-            else:
-                rc = lib.ds4f_hip_lin_decode_async(Lr, pos, dptr(d["qkv"][s]), dptr(d["z"][s]),
-                                                   dptr(d["a"][s]), dptr(d["b"][s]),
-                                                   dptr(d["cw"]), dptr(d["al"]), dptr(d["dt"]),
-                                                   dptr(d["nw"]), dptr(d["out"]), None, stream)
-            L.check(rc, f"layer {Lr} step {s}")
-
-    def capture(steps):
-        graphs = []
-        side = torch.cuda.Stream()
-        for s in steps:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=side):
-                launch_step(s, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-            graphs.append(g)
-        return graphs
-
-    graphs = capture(range(T))
+    graphs = sd.capture(range(T))
     torch.cuda.synchronize()
     for s in range(WU):
         graphs[s].replay()
@@ -253,10 +188,7 @@ def run_stack_decode(args) -> int:
         for s in range(WU, T):
             for Lr, d in enumerate(layers):
                 if d["kind"] == 2:
-                    L.check(lib.ds4f_hip_gqa_decode_async(Lr, N + s, dptr(d["q"][s]),
-                                                          dptr(d["k"][s]), dptr(d["v"][s]),
-                                                          dptr(d["qn"]), dptr(d["kn"]),
-                                                          dptr(d["out"]), None, st), "gqa")
+                    sd.launch_layer(Lr, s, st)
     n_gqa_launch = 10 * K
     gq_graph.replay()                      # warm
     torch.cuda.synchronize()
@@ -281,6 +213,7 @@ def run_stack_decode(args) -> int:
     if want_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O
+        from ds4f_hip import workloads as W
         O.lib()
         wts = {}
         for Lr, kd in enumerate(kinds):
@@ -307,9 +240,9 @@ def run_stack_decode(args) -> int:
         cpu = {"value": round(done / spent, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"{done} decode steps of the same 40-layer stack at {N} context "
                          f"(positions {N}..{N + done - 1}), C oracle gcc -O2, 1 thread, "
-                         f"{spent:.1f} s"}
+                         f"{spent:.1f} s", "host": host_cpu()}
 
-    ga.close()
+    sd.close()
     line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1,
             "steps": K, "warmup": WU, "ms_per_step": round(ms_step, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -420,7 +353,7 @@ def run_gqa_prefill(args) -> int:
         cpu = {"value": round(T / est, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"oracle gqa_body timed at {len(pos)} positions 0..{T - 1} of the same "
                          f"prefill ({sum(secs):.1f} s), linear fit integrated over the "
-                         f"{T} serial calls the reference makes (est. {est:.1f} s)"}
+                         f"{T} serial calls the reference makes (est. {est:.1f} s)", "host": host_cpu()}
     ga.close()
     line = {"metric": f"GQA causal prefill tokens/s ({T} tokens, 16q/2kv d256, 1 layer)",
             "value": round(T / (op_us * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
@@ -607,7 +540,7 @@ def run_layer_decode(args) -> int:
                 reps_cpu += 1
         cpu = {"value": round(reps_cpu / secs, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"{reps_cpu} oracle {'gqa_body' if gqa else 'lin_body'} calls of the same "
-                         f"layer shape ({secs:.1f} s)"}
+                         f"layer shape ({secs:.1f} s)", "host": host_cpu()}
     ga.close()
     what = (f"GQA decode tokens/s (1 layer, 16q/2kv d256, n_past {N})" if gqa
             else "gated delta-rule decode tokens/s (1 layer, 32 heads 128x128)")
@@ -736,7 +669,7 @@ def run_lin_prefill(args) -> int:
             done += n
         cpu = {"value": round(done / secs, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"oracle serial lin_body over the first {done} tokens of the same "
-                         f"prefill ({secs:.1f} s; per-token cost is position-independent)"}
+                         f"prefill ({secs:.1f} s; per-token cost is position-independent)", "host": host_cpu()}
     ga.close()
     line = {"metric": f"gated delta-rule prefill tokens/s ({T} tokens, 32 heads 128x128, 1 layer)",
             "value": round(T / (op_us * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
@@ -820,7 +753,7 @@ def run_mlx4_head(args) -> int:
         cpu = {"value": round(reps * rows / R / secs, 3), "unit": "matvecs/s", "cores": 1,
                "kind": "port",
                "sample": f"{reps} oracle matvecs of the first {rows} rows of the same weight "
-                         f"({secs:.1f} s), scaled to {R} rows"}
+                         f"({secs:.1f} s), scaled to {R} rows", "host": host_cpu()}
     line = {"metric": "MLX 4-bit output-head matvec (248320 x 2048) matvecs/s", "value": round(1e6 / us, 1),
             "unit": "matvecs/s", "n_gpus": 1, "steps": K, "warmup": WU,
             "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
@@ -986,7 +919,7 @@ def run_block_decode(args) -> int:
         cpu = {"value": round(done / spent, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"{done} decode steps of the same 40 whole layers at {N} context, C "
                          f"oracle gcc -O2 (layer steps incl. the 4-bit projections), 1 thread, "
-                         f"{spent:.1f} s"}
+                         f"{spent:.1f} s", "host": host_cpu()}
 
     ga.close()
     line = {"metric": "attention-block decode tokens/s (40 layers, projections included), "
@@ -1113,7 +1046,7 @@ def run_block_prefill(args) -> int:
         cpu = {"value": round(T / est, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"C oracle (gcc -O2, 1 thread) 40 whole layer steps at {len(pos)} "
                          f"positions 0..{T - 1} ({sum(secs):.1f} s), linear fit integrated "
-                         f"over the {T} serial steps of the reference's chunk (est. {est:.0f} s)"}
+                         f"over the {T} serial steps of the reference's chunk (est. {est:.0f} s)", "host": host_cpu()}
 
     ga.close()
     line = {"metric": f"attention-block prefill tokens/s ({T} tokens, 40 layers, projections "

@@ -38,14 +38,23 @@ def _err(got, ref):
 # ------------------------------------------------------------------ helpers
 def _gqa_setup(n_past, max_tokens, seed=0, layer=0):
     """A one-GQA-layer binding whose cache holds n_past bf16 rows; returns
-    (plugin, oracle kv block, weights)."""
-    kc, vc = W.gqa_cache(GQ, n_past, seed, layer)
+    (plugin, oracle kv block, weights).  Up to 8192 rows the host draws them
+    and binds; beyond, the device draws them (ds4f_hip_synth_gqa_cache, the
+    same streams) and the rows are synced to the host for the oracle."""
     cache = KvCache(1, max_tokens)
-    half = GQ.kv_heads * GQ.head_dim
-    cache.kv[0, :n_past, :half] = kc.reshape(n_past, half)
-    cache.kv[0, :n_past, half:] = vc.reshape(n_past, half)
+    if n_past <= 8192:
+        kc, vc = W.gqa_cache(GQ, n_past, seed, layer)
+        half = GQ.kv_heads * GQ.head_dim
+        cache.kv[0, :n_past, :half] = kc.reshape(n_past, half)
+        cache.kv[0, :n_past, half:] = vc.reshape(n_past, half)
+        ga = GpuAttention([2], max_tokens, cache, n_kv_tokens=n_past)
+    else:
+        from ds4f_hip.lib import check, load
+        ga = GpuAttention([2], max_tokens, cache)
+        check(load().ds4f_hip_synth_gqa_cache(0, n_past, seed, S.tid(S.GQA_KCACHE, layer),
+                                              S.tid(S.GQA_VCACHE, layer), None), "synth kv")
+        ga.sync(0, to_host=True, n_kv_tokens=n_past)
     ref_kv = cache.kv[0].copy()
-    ga = GpuAttention([2], max_tokens, cache, n_kv_tokens=n_past)
     return ga, cache, ref_kv, W.gqa_weights(GQ, seed, layer)
 
 
@@ -163,7 +172,8 @@ def test_lin_decode_4096_steps_state():
 
 
 # ------------------------------------------------------------------ GQA
-@pytest.mark.parametrize("n_past", [4096, 0, 1, 15, 16, 17, 63, 64, 65, 1000, 8191, 32768])
+@pytest.mark.parametrize("n_past", [4096, 0, 1, 15, 16, 17, 63, 64, 65, 1000, 8191, 32768,
+                                    131072])
 def test_gqa_decode_step(n_past):
     max_tokens = max(n_past + 8, 64)
     _say(f"gqa decode n_past={n_past}")
@@ -249,6 +259,8 @@ def test_prefill_entry_points_serial_semantics():
                             kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
     mx, rr = _err(out, ref)
     _say(f"gqa prefill (serial decode path) T={T}: max abs {mx:.3e} rel-rms {rr:.3e}")
+    assert mx <= ATOL
+    assert _err(kp, rk)[0] < 1e-5
     ga.close()
 
 
