@@ -61,6 +61,8 @@ static struct Plugin {
     int chunk_cap;             /* token rows (a multiple of the GEMM's M tile) */
     float *h_states;           /* pinned staging of the host chunk entry */
     size_t h_states_cap;
+    int *d_status, *h_status;  /* the prefill kernels' status word (Q35_STATUS_*) */
+    float *d_backup;           /* a delta-rule layer's state and ring before a chunk */
 } P;
 
 static void set_err(const char *fmt, ...) {
@@ -109,6 +111,12 @@ int ds4f_gpu_init(void) {
     }
     const char *f = getenv("DS4F_GPU_FAIL_AFTER");
     P.fail_countdown = f ? atoi(f) : -1;
+    if (hipMalloc((void **)&P.d_status, 256) != hipSuccess ||
+        hipHostMalloc((void **)&P.h_status, 256, hipHostMallocDefault) != hipSuccess ||
+        hipMemset(P.d_status, 0, 256) != hipSuccess) {
+        set_err("status word allocation failed");
+        return -1;
+    }
     P.ok = 1;
     return 0;
 }
@@ -122,8 +130,10 @@ static void free_binding(void) {
     if (P.d_rope) hipFree(P.d_rope);
     if (P.d_part_o) hipFree(P.d_part_o);
     if (P.d_part_ml) hipFree(P.d_part_ml);
+    if (P.d_backup) hipFree(P.d_backup);
     free(P.kind);
     free(P.slot);
+    P.d_backup = NULL;
     P.d_k = P.d_v = NULL;
     P.d_lin = P.d_conv = P.d_rope = P.d_part_o = P.d_part_ml = NULL;
     P.kind = P.slot = NULL;
@@ -137,6 +147,8 @@ void ds4f_gpu_free(void) {
     if (P.d_stage) hipFree(P.d_stage);
     if (P.h_stage) hipHostFree(P.h_stage);
     if (P.d_ws) hipFree(P.d_ws);
+    if (P.d_status) hipFree(P.d_status);
+    if (P.h_status) hipHostFree(P.h_status);
     mlx4_free();
     hipStreamDestroy(P.stream);
     memset(&P, 0, sizeof P);
@@ -440,6 +452,7 @@ int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate, const 
     p.t_tiles = P.t_tiles;
     p.heads = P.g.n_heads;
     p.kv_heads = P.g.n_kv_heads;
+    p.status = P.d_status;
     HIPCHK(q35_gqa_prefill(&p, pick(stream)));
     return 0;
 }
@@ -477,13 +490,24 @@ static int lin_prefill_launch(int L, int t0, int B, const float *qkv, const floa
                               const float *a, const float *b, const uint16_t *conv_w,
                               const float *A_log, const uint16_t *dt_bias, const uint16_t *norm_w,
                               float *out, float *qkv_post, uint16_t *xw, float *xsum, int mpad,
-                              void *stream) {
+                              void *ws, size_t ws_cap, void *stream) {
     if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
     if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;   /* src/attn_qwen.c:882 */
     if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
+    if (xw && (mpad < B || mpad % q35_mlx4_gemm_mtile() != 0 || !xsum)) {
+        set_err("lin prefill: X operand of %d rows for %d tokens", mpad, B);
+        return -1;
+    }
     size_t bytes;
     q35_lin_prefill_ws_bytes(B, P.g.n_heads, P.vh, qkv_post == NULL, &bytes);
-    if (ensure_ws(bytes) != 0) return -1;
+    if (!ws) {
+        if (ensure_ws(bytes) != 0) return -1;
+        ws = P.d_ws;
+    } else if (bytes > ws_cap) {
+        set_err("lin prefill: %d tokens need %zu workspace bytes, the static workspace holds %zu",
+                B, bytes, ws_cap);
+        return -1;
+    }
     Q35LinPrefill p;
     memset(&p, 0, sizeof p);
     p.qkv = qkv;
@@ -504,7 +528,7 @@ static int lin_prefill_launch(int L, int t0, int B, const float *qkv, const floa
     p.v_heads = P.vh;
     /* carve the workspace, each piece 256-byte aligned */
     const size_t nc = (size_t)p.n_chunks, vh = (size_t)P.vh;
-    char *w = (char *)P.d_ws;
+    char *w = (char *)ws;
 #define CARVE(dst, nfloats)                                   \
     do {                                                      \
         (dst) = (float *)w;                                   \
@@ -522,6 +546,7 @@ static int lin_prefill_launch(int L, int t0, int B, const float *qkv, const floa
     p.xw = xw;
     p.xsum = xsum;
     p.mpad = mpad;
+    p.status = P.d_status;
     HIPCHK(q35_lin_prefill(&p, pick(stream)));
     return 0;
 }
@@ -532,7 +557,7 @@ int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const flo
                                const uint16_t *norm_w, float *out, float *qkv_post,
                                void *stream) {
     return lin_prefill_launch(L, t0, B, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, out, qkv_post,
-                              NULL, NULL, 0, stream);
+                              NULL, NULL, 0, NULL, 0, stream);
 }
 
 /* ---- host-pointer entry points ----------------------------------------- */
@@ -563,6 +588,30 @@ static int download(void *d_src, size_t bytes) {
     HIPCHK(hipMemcpyAsync(P.h_stage, d_src, bytes, hipMemcpyDeviceToHost, P.stream));
     HIPCHK(hipStreamSynchronize(P.stream));
     return 0;
+}
+
+/* the status word: cleared ahead of a host entry's launches, read after */
+static int status_clear(hipStream_t st) {
+    HIPCHK(hipMemsetAsync(P.d_status, 0, sizeof(int), st));
+    return 0;
+}
+static int status_read(hipStream_t st, int *bits) {
+    HIPCHK(hipMemcpyAsync(P.h_status, P.d_status, sizeof(int), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    *bits = *P.h_status;
+    return 0;
+}
+
+int ds4f_hip_f16_status(void *stream, int clear) {
+    if (!P.ok) {
+        set_err("plugin not initialised (ds4f_gpu_init)");
+        return -1;
+    }
+    hipStream_t st = pick(stream);
+    int bits = 0;
+    if (status_read(st, &bits) != 0) return -1;
+    if (clear && bits && (status_clear(st) != 0 || hipStreamSynchronize(st) != hipSuccess)) return -1;
+    return bits;
 }
 
 int ds4f_gpu_gqa_decode(int L, int token, const float *q_gate, float *k, const float *v,
@@ -637,11 +686,28 @@ int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k, co
     const size_t ob = (size_t)B * H * D * 4, kb = (size_t)B * KVH * D * 4;
     if (upload(pc, 5, ob + kb, &dout) != 0) return fail_over(t0);
     float *d_attn = (float *)dout, *d_kpost = (float *)((char *)dout + ob);
-    if (ds4f_hip_gqa_prefill_async(L, t0, B, (const float *)dq, (const float *)dk,
+    int bits = 0;
+    if (status_clear(P.stream) != 0 ||
+        ds4f_hip_gqa_prefill_async(L, t0, B, (const float *)dq, (const float *)dk,
                                    (const float *)dv, (const uint16_t *)dqn,
                                    (const uint16_t *)dkn, d_attn, d_kpost, NULL) != 0 ||
-        download(dout, ob + kb) != 0)
+        status_read(P.stream, &bits) != 0)
         return fail_over(t0 + B);
+    if (bits & Q35_STATUS_GQA_F16) {
+        /* an operand beyond fp16 range: the tokens again on the decode
+         * kernels (bf16 cache, fp32 q and weights), in order; the prefill
+         * already wrote their cache rows, which each decode step rewrites
+         * with the same values before attending */
+        for (int b = 0; b < B; b++)
+            if (ds4f_hip_gqa_decode_async(L, t0 + b, (const float *)dq + (size_t)b * H * 2 * D,
+                                          (const float *)dk + (size_t)b * KVH * D,
+                                          (const float *)dv + (size_t)b * KVH * D,
+                                          (const uint16_t *)dqn, (const uint16_t *)dkn,
+                                          d_attn + (size_t)b * H * D,
+                                          d_kpost + (size_t)b * KVH * D, NULL) != 0)
+                return fail_over(t0 + B);
+    }
+    if (download(dout, ob + kb) != 0) return fail_over(t0 + B);
     memcpy(attn_out, P.h_stage, ob);
     memcpy(k, (char *)P.h_stage + ob, kb);
     return 0;
@@ -1244,9 +1310,16 @@ static size_t chunk_layout(int mpad, ChunkWs *ws) {
     return total;
 }
 
-static int ensure_chunk(int B, ChunkWs *ws) {
+/* The workspace grows to hold mpad = B rounded up to the GEMM's M tile;
+ * the parts' base pointers follow the capacity, and a call lays its X
+ * operand, group sums and outputs over its own mpad rows inside them.
+ * Growth frees the old buffer: a HIP graph captured over it must be
+ * captured again (a caller that captures prefill chunks makes its largest
+ * chunk first, outside the capture). */
+static int ensure_chunk(int B, ChunkWs *ws, int *mpad_out) {
     const int mt = q35_mlx4_gemm_mtile();
     const int mpad = (B + mt - 1) / mt * mt;
+    *mpad_out = mpad;
     if (mpad > P.chunk_cap) {
         if (P.d_chunk) {
             HIPCHK(hipStreamSynchronize(P.stream));
@@ -1261,13 +1334,14 @@ static int ensure_chunk(int B, ChunkWs *ws) {
     return 0;
 }
 
-/* X = [norm](x rows) (x NULL: the workspace already holds X), then
- * y = X W^T for the njobs GEMM jobs, job j writing ys[j] [B][lds[j]] */
-static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, int B,
+/* X = [norm](x rows) (x NULL: the workspace already holds X over mpad
+ * rows), then y = X W^T for the njobs GEMM jobs, job j writing ys[j]
+ * [B][lds[j]] */
+static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, int B, int mpad,
                       const Q35Mlx4GemmJob *jobs, int njobs, float *const *ys, const int *lds,
                       int accumulate, const ChunkWs *ws, hipStream_t st) {
     if (x) {
-        Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, P.chunk_cap, K, ldx};
+        Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, mpad, K, ldx, P.d_status};
         HIPCHK(q35_mlx4_xprep(&xp, st));
     }
     Q35Mlx4Gemm g;
@@ -1281,7 +1355,7 @@ static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, in
     }
     g.njobs = njobs;
     g.M = B;
-    g.Mpad = P.chunk_cap;
+    g.Mpad = mpad;
     g.K = K;
     g.accumulate = accumulate;
     HIPCHK(q35_mlx4_gemm(&g, st));
@@ -1309,7 +1383,8 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
     const LayerW *lw = &P.lw[L];
     hipStream_t st = pick(stream);
     ChunkWs ws;
-    if (ensure_chunk(B, &ws) != 0) return -1;
+    int mpad;
+    if (ensure_chunk(B, &ws, &mpad) != 0) return -1;
     const int H = P.hidden;
     /* the projections of the B normed rows */
     const int outs[4] = {kind == DS4F_LAYER_GQA ? CH_Q : CH_QKV, kind == DS4F_LAYER_GQA ? CH_K : CH_Z,
@@ -1320,7 +1395,7 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
         ys[j] = ws.out[outs[j]];
         lds[j] = (int)ch_width(outs[j]);
     }
-    if (chunk_gemm(states, H, lw->in_norm, H, B, lw->gj, lw->njobs, ys, lds, 0, &ws, st) != 0)
+    if (chunk_gemm(states, H, lw->in_norm, H, B, mpad, lw->gj, lw->njobs, ys, lds, 0, &ws, st) != 0)
         return -1;
     /* the core over the chunk */
     int core_out;
@@ -1333,7 +1408,7 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
         /* the gated norm writes the output GEMM's X operand directly */
         if (lin_prefill_launch(L, t0, B, ws.out[CH_QKV], ws.out[CH_Z], ws.out[CH_A], ws.out[CH_B],
                                lw->conv_w, lw->A_log, lw->dt_bias, lw->norm_w, ws.out[CH_LO], NULL,
-                               ws.xw, ws.xsum, P.chunk_cap, st) != 0)
+                               ws.xw, ws.xsum, mpad, NULL, 0, st) != 0)
             return -1;
         core_out = -1;
     }
@@ -1341,8 +1416,8 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
     float *yo[1] = {states};
     const int ldo[1] = {H};
     const int K = (int)ch_width(kind == DS4F_LAYER_GQA ? CH_AO : CH_LO);
-    return chunk_gemm(core_out >= 0 ? ws.out[core_out] : NULL, K, NULL, K, B, lw->gj + lw->njobs, 1,
-                      yo, ldo, 1, &ws, st);
+    return chunk_gemm(core_out >= 0 ? ws.out[core_out] : NULL, K, NULL, K, B, mpad,
+                      lw->gj + lw->njobs, 1, yo, ldo, 1, &ws, st);
 }
 
 int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {
@@ -1370,10 +1445,41 @@ int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {
         P.h_states_cap = bytes;
     }
     if (ensure_stage(bytes, 0) != 0) return fail_over(t0);
+    const int lin = P.kind[L] == DS4F_LAYER_LINEAR;
+    const size_t sb = lin_floats() * sizeof(float), cb = conv_floats() * sizeof(float);
+    if (lin && !P.d_backup && hipMalloc((void **)&P.d_backup, sb + cb) != hipSuccess) {
+        set_err("chunk: state backup allocation failed");
+        return fail_over(t0);
+    }
     for (int b = 0; b < B; b++) memcpy((char *)P.h_states + b * row, states[b], row);
-    if (hipMemcpyAsync(P.d_stage, P.h_states, bytes, hipMemcpyHostToDevice, P.stream) != hipSuccess ||
-        ds4f_hip_attn_chunk_async(L, t0, B, (float *)P.d_stage, NULL) != 0 ||
-        hipMemcpyAsync(P.h_states, P.d_stage, bytes, hipMemcpyDeviceToHost, P.stream) != hipSuccess ||
+    float *d_states = (float *)P.d_stage;
+    int bits = 0;
+    /* a delta-rule layer's state and ring are kept until the chunk is known
+     * to be good: a recomputation starts from them */
+    if ((lin && (hipMemcpyAsync(P.d_backup, layer_lin(P.slot[L]), sb, hipMemcpyDeviceToDevice,
+                                P.stream) != hipSuccess ||
+                 hipMemcpyAsync((char *)P.d_backup + sb, layer_conv(P.slot[L]), cb,
+                                hipMemcpyDeviceToDevice, P.stream) != hipSuccess)) ||
+        hipMemcpyAsync(d_states, P.h_states, bytes, hipMemcpyHostToDevice, P.stream) != hipSuccess ||
+        status_clear(P.stream) != 0 || ds4f_hip_attn_chunk_async(L, t0, B, d_states, NULL) != 0 ||
+        status_read(P.stream, &bits) != 0)
+        return fail_over(t0);
+    if (bits) {
+        /* a GEMM or attention operand beyond fp16 range: the chunk again as
+         * B layer steps on the decode kernels (fp32 activations, bf16 cache),
+         * from the states and the layer state the chunk started from */
+        if ((lin && (hipMemcpyAsync(layer_lin(P.slot[L]), P.d_backup, sb, hipMemcpyDeviceToDevice,
+                                    P.stream) != hipSuccess ||
+                     hipMemcpyAsync(layer_conv(P.slot[L]), (char *)P.d_backup + sb, cb,
+                                    hipMemcpyDeviceToDevice, P.stream) != hipSuccess)) ||
+            hipMemcpyAsync(d_states, P.h_states, bytes, hipMemcpyHostToDevice, P.stream) !=
+                hipSuccess)
+            return fail_over(t0);
+        for (int b = 0; b < B; b++)
+            if (ds4f_hip_attn_step_async(L, t0 + b, d_states + (size_t)b * P.hidden, NULL) != 0)
+                return fail_over(t0);
+    }
+    if (hipMemcpyAsync(P.h_states, d_states, bytes, hipMemcpyDeviceToHost, P.stream) != hipSuccess ||
         hipStreamSynchronize(P.stream) != hipSuccess)
         return fail_over(t0);
     for (int b = 0; b < B; b++) memcpy(states[b], (char *)P.h_states + b * row, row);

@@ -117,6 +117,8 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
     for (int hh = 0; hh < 4; hh++) {
         const int head = 4 * w + hh, g = head / G, hl = head % G;
         const float4 y = q35_norm_rope_head(xq[hh], wq, rc, rs, lane);
+        q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(y.x) || q35_f16_over(y.y) ||
+                                                        q35_f16_over(y.z) || q35_f16_over(y.w));
         uint16_t *dst = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + qp) * D + d0;
         const uint2 pk = make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
                                     (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
@@ -126,6 +128,8 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
 #pragma unroll
         for (int g = 0; g < 2; g++) {
             const float4 y = q35_norm_rope_head(xk[g], wk, rc, rs, lane);
+            q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(y.x) || q35_f16_over(y.y) ||
+                                                            q35_f16_over(y.z) || q35_f16_over(y.w));
             if (p.k_post)
                 *reinterpret_cast<float4 *>(p.k_post + ((size_t)b * p.kv_heads + g) * D + d0) = y;
             uint16_t *dst = p.kw + kw_index(g, p.kbt, pos, d0);
@@ -157,6 +161,8 @@ __global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (pos >= p.t0 && pos < p.t0 + p.B)
             v = *reinterpret_cast<const float4 *>(p.v_in + ((size_t)(pos - p.t0) * p.kv_heads + g) * D + c4);
+        q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(v.x) || q35_f16_over(v.y) ||
+                                                        q35_f16_over(v.z) || q35_f16_over(v.w));
         sv[r][c4] = v.x;
         sv[r][c4 + 1] = v.y;
         sv[r][c4 + 2] = v.z;
@@ -195,6 +201,7 @@ __global__ void prefix_kernel(Q35GqaPrefill p, int n_rows) {
     if (pos < p.t0) {
         kf = q35_bf2f(p.kt[q35_k_index(g, pos, d, p.t_tiles)]);
         vf = q35_bf2f(p.vt[q35_v_index(g, pos, d, p.t_tiles)]);
+        q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(kf) || q35_f16_over(vf));
     }
     p.kw[kw_index(g, p.kbt, pos, d)] = f16_bits(kf);
     p.vw[vw_index(g, p.kbt, pos >> 5, d, v_slot(pos & 31))] = f16_bits(vf);

@@ -661,6 +661,7 @@ __global__ __launch_bounds__(256) void gnorm_kernel(Q35LinPrefill p) {
         *reinterpret_cast<float2 *>(p.out + off) = y;
         return;
     }
+    q35_f16_guard(p.status, Q35_STATUS_GEMM_F16, q35_f16_over(y.x) || q35_f16_over(y.y));
     /* The chunk GEMM's X operand instead: quad lanes 4k..4k+3 hold word k
      * of the head's 16 (values 2i, 2i + 1 in quad lane i); every lane of the
      * quad gathers the word, lane 0 stores its hi granule, lane 1 its lo.
@@ -708,6 +709,8 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     if (p.B < 1 || p.t0 < 0 || p.v_heads != 2 * p.k_heads || p.v_heads % 8 != 0 ||
         p.k_heads % 2 != 0 || rows % 1024 != 0 || p.n_chunks != (p.B + C - 1) / C)
         return hipErrorInvalidValue;
+    /* checked before any launch: the kernels advance the ring and state in place */
+    if (p.xw && (p.mpad < p.B || p.mpad % Q35_XW_ROWS != 0 || !p.xsum)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(conv_kernel, dim3(rows / 1024, (p.B + CT - 1) / CT), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -715,7 +718,7 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(SCAN_THREADS), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (p.xw && (p.mpad < p.B || p.mpad % Q35_XW_ROWS != 0 || !p.xsum)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(gnorm_kernel, dim3(p.v_heads / 4, p.B), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
+

@@ -118,6 +118,10 @@ __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
                     e[j] = e[j] / r * q35_bf2f((uint16_t)(ww[j >> 1] >> (16 * (j & 1))));
             }
         }
+        bool over = false;
+#pragma unroll
+        for (int j = 0; j < 8; j++) over = over || q35_f16_over(e[j]);
+        q35_f16_guard(p.status, Q35_STATUS_GEMM_F16, over);
         f16x8_t hi, lo;
         float s = 0.0f;
 #pragma unroll

@@ -181,6 +181,18 @@ __device__ __forceinline__ void q35_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+/* fp16 range guard.  A float of magnitude 65520 or more rounds to an fp16
+ * infinity.  A kernel that stores values as fp16 operands passes each
+ * value's check here; any lane whose value is out of range sets `bit` in
+ * the status word (device memory the host reads after the launches), so the
+ * host can recompute the affected work on a path without fp16 operands.
+ * Out-of-range values never occur in normal activations; the check costs a
+ * compare per value and the atomic only runs when one is out of range. */
+__device__ __forceinline__ bool q35_f16_over(float x) { return fabsf(x) >= 65520.0f; }
+__device__ __forceinline__ void q35_f16_guard(int *status, int bit, bool over) {
+    if (over && status) atomicOr(status, bit);
+}
+
 /* exp on the hardware 2^x instruction (v_exp_f32), ~1e-7 relative error:
  * used for softmax weights, whose reference-order expf only matters to
  * float rounding. */

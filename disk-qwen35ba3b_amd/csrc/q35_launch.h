@@ -25,6 +25,12 @@
 extern "C" {
 #endif
 
+/* Bits of the status word the prefill kernels set (q35_f16_guard): a value
+ * out of fp16 range met by the GQA prefill's operand conversion, or by the
+ * chunk GEMM's X operand (its X prep or the delta-rule gated norm). */
+#define Q35_STATUS_GQA_F16  1
+#define Q35_STATUS_GEMM_F16 2
+
 /* ---- gated delta-rule decode (kd = vd = 128) ---- */
 typedef struct Q35LinDecode {
     const float *qkv, *z, *a, *b;
@@ -61,6 +67,7 @@ typedef struct Q35LinPrefill {
     uint16_t *xw;
     float *xsum;
     int mpad;
+    int *status;                   /* Q35_STATUS_GEMM_F16 (xw path), or NULL */
 } Q35LinPrefill;
 /* workspace bytes, post included when with_post != 0 */
 void q35_lin_prefill_ws_bytes(int B, int k_heads, int v_heads, int with_post, size_t *bytes);
@@ -104,6 +111,7 @@ typedef struct Q35GqaPrefill {
     float *k_post;                 /* optional [B][KVH][D] */
     int t0, B, t_tiles, heads, kv_heads;
     int nqb, kbt;
+    int *status;                   /* Q35_STATUS_GQA_F16, or NULL */
 } Q35GqaPrefill;
 void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *qw, size_t *kw, size_t *vw);
 hipError_t q35_gqa_prefill(const Q35GqaPrefill *p, hipStream_t stream);
@@ -170,6 +178,7 @@ typedef struct Q35Mlx4Xprep {
     uint16_t *xw;                  /* Mpad * K * 2 halfs: hi / lo blocks per (64-row tile, group) */
     float *xsum;                   /* [K/64][Mpad] */
     int M, Mpad, K, ldx;
+    int *status;                   /* Q35_STATUS_GEMM_F16, or NULL */
 } Q35Mlx4Xprep;
 typedef struct Q35Mlx4SB {
     float s, b;                    /* 16 scale, bias - 16 scale */

@@ -67,6 +67,7 @@ _SIGS = {
     "ds4f_hip_synth_lin_state": ([_i, _d, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_conv_history": ([_i, _i, _u64, _u64, _vp], _i),
     "ds4f_gpu_last_error": ([], ctypes.c_char_p),
+    "ds4f_hip_f16_status": ([_vp, _i], _i),
     "ds4f_gpu_attn_weights": ([_i, ctypes.POINTER(LayerW)], _i),
     "ds4f_gpu_attn_step": ([_i, _i, _vp], _i),
     "ds4f_hip_attn_step_async": ([_i, _i, _vp, _vp], _i),

@@ -267,8 +267,26 @@ int ds4f_hip_attn_step_async(int L, int token, float *state, void *stream);
 int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states);
 /* The same with the states in device memory, [B][hidden] contiguous,
  * enqueued on `stream`.  Allocates its workspace on first use or growth
- * (not capturable then). */
+ * (not capturable then); growth frees the previous workspace, so a HIP
+ * graph captured before it must be captured again -- a caller that
+ * captures chunks runs its largest chunk once before capturing. */
 int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream);
+
+/* The prefill paths compute with fp16 operands (the GQA prefill's q, k, v
+ * and the chunk GEMM's X), which hold magnitudes below 65520; the
+ * reference is fp32 throughout (src/attn_qwen.c:328-386, :1222-1231).
+ * Their kernels set bits of a status word when a value is out of that
+ * range: 1 = a GQA prefill operand, 2 = a chunk GEMM X operand.  The host
+ * entries ds4f_gpu_gqa_prefill and ds4f_gpu_attn_chunk clear the word
+ * before their launches, read it after, and recompute a flagged call on
+ * the decode kernels (fp32 activations, bf16 cache) in token order, from
+ * the state the call started from, so their results stay exact.  Callers
+ * of the device-pointer prefills (ds4f_hip_gqa_prefill_async,
+ * ds4f_hip_attn_chunk_async) read the word here: this synchronises
+ * `stream` (NULL: the plugin's stream) and returns the bits set since the
+ * last clear (0: every fp16 operand was in range; -1 on error); clear != 0
+ * clears them.  Outputs of a flagged device-pointer call are not valid. */
+int ds4f_hip_f16_status(void *stream, int clear);
 
 /* Last error text of the plugin (static storage). */
 const char *ds4f_gpu_last_error(void);

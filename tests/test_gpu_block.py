@@ -330,3 +330,127 @@ def test_four_layer_stack_one_chunk():
             assert mx <= ATOL
     finally:
         ga.close()
+
+
+def test_engine_order_chunks_then_decode():
+    """A prompt in the engine's order (src/main.c:583-665): three chunks
+    (64, 64, 37 tokens) from position 0, each run through every layer of a
+    lin-lin-lin-GQA stack before the next chunk, the hidden states passed
+    from layer to layer; then three decode tokens through the same layers
+    (src/main.c:924-957) on the state the chunks left on the device.  The
+    oracle runs its chunks and layer steps in the same order.  The host only
+    syncs the device state at the end, where the delta-rule states, the
+    conv rings and the GQA cache rows are compared with the oracle's."""
+    kinds = [1, 1, 1, 2]
+    chunks = (64, 64, 37)
+    n_tok = sum(chunks) + 3
+    ga, ref, ws = _stack(kinds, 0, 0, 256, seed=5)
+    try:
+        t = 0
+        for n, B in enumerate(chunks):
+            st_g = np.stack([W.hidden_state(HID, 5, 2000 + t + b) for b in range(B)])
+            st_o = st_g.copy()
+            for L, kind in enumerate(kinds):
+                st_g = ga.attn_chunk(L, t, st_g)
+                if kind == 2:
+                    st_o = O.gqa_chunk(ref[L], t, st_o, ws[L], GQ.heads, GQ.kv_heads, GQ.head_dim)
+                    ref[L][t:t + B] = SY.bf16_round(ref[L][t:t + B])   # the device's stored rows
+                else:
+                    ring, S = ref[L]
+                    st_o = O.lin_chunk(ring, S, t, st_o, ws[L], LG.k_heads, LG.v_heads, LG.kd,
+                                       LG.vd)
+            mx, rr = _err(st_g, st_o)
+            _say(f"engine order: chunk {n} (t0 {t}, B {B}) through 4 layers: max scaled err "
+                 f"{mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+            t += B
+        for s in range(3):
+            st_g = st_o = W.hidden_state(HID, 5, 2500 + s)
+            for L, kind in enumerate(kinds):
+                st_g = ga.attn_step(L, t, st_g)
+                st_o = _oracle_layer(kind, ref[L], ws[L], t, st_o)
+                if kind == 2:
+                    ref[L][t] = SY.bf16_round(ref[L][t])
+            mx, rr = _err(st_g, st_o)
+            _say(f"engine order: decode token {t}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+            t += 1
+        assert t == n_tok
+        ga.sync(-1, to_host=True, n_kv_tokens=n_tok)
+        for L, kind in enumerate(kinds):
+            if kind == 2:
+                # rows of k / v projected by the chunk GEMM or the matvec,
+                # bf16 on both sides: equal up to a bf16 rounding step
+                d = np.abs(ga.cache.kv[L, :n_tok] - ref[L][:n_tok])
+                lim = 2.0 ** -7 * np.abs(ref[L][:n_tok]) + 1e-4
+                _say(f"engine order: GQA rows max |d| {d.max():.3e}, "
+                     f"{int((d > 0).sum())} of {d.size} differ")
+                assert (d <= lim).all()
+            else:
+                ring, S = ref[L]
+                srel = np.sqrt(((ga.cache.lin[L] - S) ** 2).sum() / (S ** 2).sum())
+                rmax = np.abs(ga.cache.conv[L] - ring).max() / np.abs(ring).max()
+                _say(f"engine order: layer {L} state rel {srel:.3e}, ring max rel {rmax:.3e}")
+                assert srel <= 1e-4 and rmax <= 1e-4
+    finally:
+        ga.close()
+
+
+@pytest.mark.parametrize("kind", [2, 1])
+def test_chunk_fp16_range_falls_back(kind):
+    """An input_layernorm weight of 2^18 (exact in bf16) makes one column
+    of the normed rows exceed fp16 range: the chunk GEMM's X prep flags it
+    (status bit 2) and the host chunk entry recomputes the chunk as layer
+    steps on the decode kernels from the state it started from (the
+    delta-rule state and ring restored).  The result is bit for bit that of
+    B ds4f_gpu_attn_step calls on a fresh binding of the same state, and
+    matches the oracle's chunk to a relative RMS of 2e-3 (the activations
+    reach about 1e5, so the bf16 cache rows' rounding is large in absolute
+    terms)."""
+    t0, B = 5, 24
+
+    def planted():
+        ga, ref, ws = _stack([kind], t0, t0, 128, seed=6)
+        w = ws[0]
+        nw = w.in_norm.copy()
+        nw[5] = SY.bf16_bits(np.array([2.0 ** 18], np.float32))[0]
+        w.in_norm = nw
+        ga.set_layer_weights(0, w)
+        return ga, ref, w
+
+    states = np.stack([W.hidden_state(HID, 6, 3300 + b) for b in range(B)])
+    ga, ref, w = planted()
+    try:
+        assert ga.lib.ds4f_hip_f16_status(None, 1) >= 0
+        got = ga.attn_chunk(0, t0, states)
+        bits = ga.lib.ds4f_hip_f16_status(None, 1)
+        if kind == 1:
+            ga.sync(0, to_host=True)
+            dev_S = ga.cache.lin[0].copy()
+    finally:
+        ga.close()
+    ga2, _, _ = planted()
+    try:
+        steps = np.stack([ga2.attn_step(0, t0 + b, states[b]) for b in range(B)])
+        if kind == 1:
+            ga2.sync(0, to_host=True)
+            step_S = ga2.cache.lin[0].copy()
+    finally:
+        ga2.close()
+    if kind == 2:
+        exp = O.gqa_chunk(ref[0], t0, states, w, GQ.heads, GQ.kv_heads, GQ.head_dim)
+    else:
+        ring, S = ref[0]
+        exp = O.lin_chunk(ring, S, t0, states, w, LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+    assert np.isfinite(got).all()
+    mx, rr = _err(got, exp)
+    _say(f"chunk kind {kind} with an fp16-range plant: status {bits}, |exp| max "
+         f"{np.abs(exp).max():.3e}, against the oracle: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+    assert bits & 2
+    assert np.array_equal(got, steps)
+    assert rr <= ATOL
+    if kind == 1:
+        srel = np.sqrt(((dev_S - S) ** 2).sum() / (S ** 2).sum())
+        _say(f"  state rel {srel:.3e}")
+        assert np.array_equal(dev_S, step_S)
+        assert srel <= 1e-4
