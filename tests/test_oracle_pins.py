@@ -5,7 +5,9 @@ and it does not compile in this image, so the oracle is pinned by:
   * the double-precision model in f64_model.py (independent statement),
   * closed forms and invariants the mathematics fixes,
   * known-answer vectors of the input generator,
-  * the committed fixtures in tests/golden/ (regenerated by its script).
+  * the reference's own known answers for the MLX 4-bit format and matvec
+    (tests/test_kernels.c:357-446 of the reference, restated as values in
+    the MLX 4-bit tests below).
 """
 import numpy as np
 import pytest
