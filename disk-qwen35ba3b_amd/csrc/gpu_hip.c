@@ -61,6 +61,7 @@ static struct Plugin {
     int chunk_cap;             /* token rows (a multiple of the GEMM's M tile) */
     float *h_states;           /* pinned staging of the host chunk entry */
     size_t h_states_cap;
+    int scratch_rc;            /* q35_lin_scratch_init's result at init */
     int *d_status, *h_status;  /* the prefill kernels' status word (Q35_STATUS_*) */
     float *d_backup;           /* a delta-rule layer's state and ring before a chunk */
 } P;
@@ -111,6 +112,9 @@ int ds4f_gpu_init(void) {
     }
     const char *f = getenv("DS4F_GPU_FAIL_AFTER");
     P.fail_countdown = f ? atoi(f) : -1;
+    /* the device address of the no-allocation entry's static workspace, on
+     * this device; a failure here only disables that entry */
+    P.scratch_rc = (int)q35_lin_scratch_init();
     if (hipMalloc((void **)&P.d_status, 256) != hipSuccess ||
         hipHostMalloc((void **)&P.h_status, 256, hipHostMallocDefault) != hipSuccess ||
         hipMemset(P.d_status, 0, 256) != hipSuccess) {
@@ -558,6 +562,28 @@ int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv, const flo
                                void *stream) {
     return lin_prefill_launch(L, t0, B, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, out, qkv_post,
                               NULL, NULL, 0, NULL, 0, stream);
+}
+
+int ds4f_hip_lin_prefill_noalloc(int L, int t0, int B, const float *qkv, const float *z,
+                                 const float *a, const float *b, const uint16_t *conv_w,
+                                 const float *A_log, const uint16_t *dt_bias,
+                                 const uint16_t *norm_w, float *out, float *qkv_post,
+                                 void *stream) {
+    if (check_layer(L, DS4F_LAYER_LINEAR) != 0) return -1;
+    if (t0 >= 0 && t0 < P.g.max_tokens && B > Q35_LIN_NOALLOC_MAX_B &&
+        (B < P.g.max_tokens - t0 ? B : P.g.max_tokens - t0) > Q35_LIN_NOALLOC_MAX_B) {
+        set_err("lin prefill (no allocation): %d tokens exceed the maximum of %d", B,
+                Q35_LIN_NOALLOC_MAX_B);
+        return -1;
+    }
+    void *ws = q35_lin_scratch();
+    if (P.scratch_rc != (int)hipSuccess || !ws) {
+        set_err("lin prefill (no allocation): static workspace address unavailable (%s)",
+                hipGetErrorString((hipError_t)P.scratch_rc));
+        return -1;
+    }
+    return lin_prefill_launch(L, t0, B, qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, out, qkv_post,
+                              NULL, NULL, 0, ws, Q35_LIN_SCRATCH_BYTES, stream);
 }
 
 /* ---- host-pointer entry points ----------------------------------------- */

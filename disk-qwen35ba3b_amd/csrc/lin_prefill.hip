@@ -722,3 +722,37 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     return hipGetLastError();
 }
 
+/* ---- the workspace of the no-allocation entry point ---------------------
+ * One file-scope device array: every GPU the library runs on holds its own
+ * copy until the process ends, and every no-allocation call on that GPU
+ * uses it (its contents are the last call's; each call writes every part
+ * it reads before reading it, so nothing needs clearing).  In host code the
+ * name `scratch` is a host-side stand-in, not a device address: the device
+ * address comes from hipGetSymbolAddress, taken once per device with that
+ * device current (q35_lin_scratch_init, called by the plugin's init) and
+ * kept per device in scratch_dev. */
+static __device__ __align__(256) unsigned char scratch[Q35_LIN_SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEV = 64;
+void *scratch_dev[SCRATCH_MAX_DEV];
+}  // namespace
+
+extern "C" hipError_t q35_lin_scratch_init(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= SCRATCH_MAX_DEV) return hipErrorInvalidDevice;
+    if (scratch_dev[dev]) return hipSuccess;
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    scratch_dev[dev] = ptr;
+    return hipSuccess;
+}
+
+extern "C" void *q35_lin_scratch(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEV) return nullptr;
+    return scratch_dev[dev];
+}

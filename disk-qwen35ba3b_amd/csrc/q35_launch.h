@@ -72,6 +72,16 @@ typedef struct Q35LinPrefill {
 /* workspace bytes, post included when with_post != 0 */
 void q35_lin_prefill_ws_bytes(int B, int k_heads, int v_heads, int with_post, size_t *bytes);
 hipError_t q35_lin_prefill(const Q35LinPrefill *p, hipStream_t stream);
+/* The static device workspace of the no-allocation prefill entry: 8 MiB,
+ * one per GPU, for chunks of at most Q35_LIN_NOALLOC_MAX_B tokens (6.1 MiB
+ * at 16 key / 32 value heads with the post rows in the workspace).
+ * q35_lin_scratch_init takes its device address on the current device
+ * (once per device); q35_lin_scratch returns it for the current device
+ * (NULL before the init). */
+#define Q35_LIN_SCRATCH_BYTES ((size_t)8 << 20)
+#define Q35_LIN_NOALLOC_MAX_B 128
+hipError_t q35_lin_scratch_init(void);
+void *q35_lin_scratch(void);
 
 /* ---- GQA split-K decode (head_dim 256, 8 q heads per kv head) ---- */
 typedef struct Q35GqaDecode {

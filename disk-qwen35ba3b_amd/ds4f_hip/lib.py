@@ -60,6 +60,7 @@ _SIGS = {
     "ds4f_hip_gqa_decode_async": ([_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "ds4f_hip_gqa_prefill_async": ([_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "ds4f_hip_lin_prefill_async": ([_i, _i, _i] + [_vp] * 11, _i),
+    "ds4f_hip_lin_prefill_noalloc": ([_i, _i, _i] + [_vp] * 11, _i),
     "ds4f_hip_lin_decode_async": ([_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp], _i),
     "ds4f_hip_synth": ([_vp, _i64, _i, _i, _d, _d, _u64, _u64, _vp], _i),

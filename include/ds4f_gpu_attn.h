@@ -150,6 +150,23 @@ int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv,
                                const uint16_t *conv_w, const float *A_log,
                                const uint16_t *dt_bias, const uint16_t *norm_w,
                                float *out, float *qkv_post, void *stream);
+/* The delta-rule prefill of ds4f_hip_lin_prefill_async with no allocation:
+ * no counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  The kernels and the results are those of
+ * ds4f_hip_lin_prefill_async; the workspace is one static 8 MiB device array
+ * per GPU instead of the plugin's grow-only buffer, so a call takes at most
+ * 128 tokens (two 64-token chunks; 6.1 MiB of workspace at 16 key / 32
+ * value heads).  A larger B (after the clip at max_tokens), or a geometry
+ * whose workspace exceeds the array, returns -1 (error text in
+ * ds4f_gpu_last_error) with nothing launched.  Every call on one GPU uses
+ * that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race. */
+int ds4f_hip_lin_prefill_noalloc(int L, int t0, int B, const float *qkv,
+                                 const float *z, const float *a, const float *b,
+                                 const uint16_t *conv_w, const float *A_log,
+                                 const uint16_t *dt_bias, const uint16_t *norm_w,
+                                 float *out, float *qkv_post, void *stream);
 int ds4f_hip_lin_decode_async(int L, int token, const float *qkv,
                               const float *z, const float *a, const float *b,
                               const uint16_t *conv_w, const float *A_log,
