@@ -116,7 +116,8 @@ def main() -> int:
                                                                     "lin_prefill", "hbm_copy",
                                                                     "gqa_decode", "lin_decode",
                                                                     "mlx4_head",
-                                                                    "block_decode", "block_prefill"])
+                                                                    "block_decode", "block_prefill",
+                                                                    "launch_floor"])
     ap.add_argument("--tokens", type=int, default=4096, help="prefill length (prefill workloads)")
     ap.add_argument("--npast", type=int, default=4096, help="cached positions (gqa_decode)")
     ap.add_argument("--rotate", type=int, default=0,
@@ -141,7 +142,52 @@ def main() -> int:
         return run_block_decode(args)
     if args.workload == "block_prefill":
         return run_block_prefill(args)
+    if args.workload == "launch_floor":
+        return run_launch_floor(args)
     return run_stack_decode(args)
+
+
+def run_launch_floor(args) -> int:
+    """The fixed cost of a kernel boundary: n launches of an empty kernel
+    captured as one HIP graph, replayed between two events, for the launch
+    shapes of the decode step (the delta-rule layer's 32 x 1024, the GQA
+    split's 256 x 512 and merge's 256 x 256) and a single wave."""
+    import torch
+
+    from ds4f_hip import lib as L
+
+    lib = L.load()
+    L.check(lib.ds4f_gpu_init(), "init")
+    torch.cuda.init()
+    n = 200
+    shapes = [(32, 1024), (256, 512), (256, 256), (1, 64)]
+    res = []
+    for grid, block in shapes:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        with torch.cuda.graph(g, stream=side):
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            L.check(lib.ds4f_hip_launch_floor(n, grid, block, st), "launch floor")
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(max(3, args.steps // 10)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / n
+            best = us if best is None else min(best, us)
+        res.append({"grid": grid, "block": block, "us_per_launch": round(best, 3)})
+        del g
+    line = {"metric": "empty-kernel launch floor in a HIP graph", "value": res[0]["us_per_launch"],
+            "unit": "us/launch", "n_gpus": 1, "steps": n, "warmup": 3, "higher_is_better": False,
+            "config": {"workload": "launch_floor", "launches_per_graph": n},
+            "shapes": res}
+    print(json.dumps(line), flush=True)
+    return 0
 
 
 def run_stack_decode(args) -> int:

@@ -772,6 +772,12 @@ int ds4f_gpu_lin_prefill(int L, int t0, int B, float *qkv, const float *z, const
 
 /* ---- synthetic state ---------------------------------------------------- */
 
+int ds4f_hip_launch_floor(int n, int grid, int block, void *stream) {
+    if (ds4f_gpu_init() != 0) return -1;
+    HIPCHK(q35_empty_kernels(n, grid, block, pick(stream)));
+    return 0;
+}
+
 int ds4f_hip_synth(void *dst, int64_t n, int dtype, int dist, double p0, double p1,
                    uint64_t seed, uint64_t tid, void *stream) {
     if (ds4f_gpu_init() != 0) return -1;

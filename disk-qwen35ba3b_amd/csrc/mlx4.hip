@@ -204,11 +204,14 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
         q35_uniform_ptr(j.y), 0, p.accumulate ? 4 * R : 0, Q35_BUF_DW3);
     for (int r0 = RP * wave; r0 < R; r0 += RP * nwaves) {
         /* the next rows and these rows' y are requested before these rows
-         * are consumed */
+         * are consumed.  A wave's last rows request nothing more: loads past
+         * R read zeros without a memory access, but the wave would still wait
+         * for them before it retires. */
         const float yv = __uint_as_float(
             __builtin_amdgcn_raw_buffer_load_b32(yrs, lane < RP ? 4 * (r0 + lane) : 4 * R, 0, 0));
+        const bool more = r0 + RP * nwaves < R;
         Rows nxt;
-        load_rows(r0 + RP * nwaves, nxt);
+        if (more) load_rows(r0 + RP * nwaves, nxt);
         float part[RP];
 #pragma unroll
         for (int u = 0; u < RP; u++) {
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
             t = lane == u ? tu : t;
         }
         if (lane < RP && r0 + lane < R) j.y[r0 + lane] = p.accumulate ? yv + t : t;
-        cur = nxt;
+        if (more) cur = nxt;
     }
 }
 

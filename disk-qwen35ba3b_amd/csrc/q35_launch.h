@@ -146,6 +146,9 @@ hipError_t q35_synth_state(float *state, int heads, int kd, int vd, double sigma
 hipError_t q35_synth_conv(float *ring, int rows, int token, uint64_t seed, uint64_t tid,
                           hipStream_t stream);
 
+/* n launches of an empty kernel of `grid` workgroups of `block` threads */
+hipError_t q35_empty_kernels(int n, int grid, int block, hipStream_t stream);
+
 /* ---- MLX 4-bit affine matvec (src/kernels.c:104-219) ---- *
  * y[R] = W[R x C] x, W as U32 nibble words + BF16 scale / bias per 64
  * elements (biases may be NULL).  One job: the inline pointers, jobs NULL.

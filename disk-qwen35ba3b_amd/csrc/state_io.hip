@@ -167,3 +167,21 @@ extern "C" hipError_t q35_synth_conv(float *ring, int rows, int token, uint64_t 
                        token, seed, tid);
     return hipGetLastError();
 }
+
+/* ---- launch floor ---------------------------------------------------------
+ * A kernel that does nothing: n launches of it in a row (in a HIP graph)
+ * time the fixed cost of a kernel boundary on this GPU, the floor under
+ * every latency-bound launch of the decode step. */
+namespace {
+__global__ void empty_kernel() {}
+}  // namespace
+
+extern "C" hipError_t q35_empty_kernels(int n, int grid, int block, hipStream_t stream) {
+    if (n < 0 || grid < 1 || block < 1 || block > 1024) return hipErrorInvalidValue;
+    for (int i = 0; i < n; i++) {
+        hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(block), 0, stream);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}

@@ -12,7 +12,8 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libds4f_attn_hip.so")
+# DS4F_HIP_LIB names another build of the plugin to load (comparing builds)
+LIB_PATH = os.environ.get("DS4F_HIP_LIB") or os.path.join(HERE, "libds4f_attn_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "ds4f_gpu_attn.h")
 
 LAYER_NONE, LAYER_LINEAR, LAYER_GQA = 0, 1, 2
@@ -64,6 +65,7 @@ _SIGS = {
     "ds4f_hip_lin_decode_async": ([_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp], _i),
     "ds4f_hip_synth": ([_vp, _i64, _i, _i, _d, _d, _u64, _u64, _vp], _i),
+    "ds4f_hip_launch_floor": ([_i, _i, _i, _vp], _i),
     "ds4f_hip_synth_gqa_cache": ([_i, _i, _u64, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_lin_state": ([_i, _d, _u64, _u64, _vp], _i),
     "ds4f_hip_synth_conv_history": ([_i, _i, _u64, _u64, _vp], _i),
@@ -105,6 +107,8 @@ def load():
         import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         for name, (args, res) in _SIGS.items():
+            if os.environ.get("DS4F_HIP_LIB") and not hasattr(L, name):
+                continue          # another build, without this entry
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = res

@@ -192,6 +192,13 @@ int ds4f_hip_synth_lin_state(int L, double sigma, uint64_t seed, uint64_t tid,
 int ds4f_hip_synth_conv_history(int L, int token, uint64_t seed, uint64_t tid,
                                 void *stream);
 
+/* ---- measurement ------------------------------------------------------ *
+ * Enqueue n launches of a kernel that does nothing (grid workgroups of
+ * block threads) on `stream`: captured in a HIP graph, they time the fixed
+ * cost of a kernel boundary, the floor of every latency-bound launch.  No
+ * counterpart in the reference. */
+int ds4f_hip_launch_floor(int n, int grid, int block, void *stream);
+
 /* ---- the MLX-4bit matvecs of include/ds4f/gpu.h (:29-54) --------------- *
  * y = W x for an MLX 4-bit affine [R x C] weight in the layout of
  * ds4f_mlx4_matvec (src/kernels.c:104-219): U32 words of 8 nibbles, low
