@@ -75,6 +75,11 @@ static void set_err(const char *fmt, ...) {
 
 const char *ds4f_gpu_last_error(void) { return P.err; }
 
+/* for the plugin's other translation units (trunk.c) */
+__attribute__((visibility("hidden"))) void ds4f_plugin_set_err(const char *msg) {
+    set_err("%s", msg);
+}
+
 static void mlx4_free(void);
 static void layers_free(void);
 

@@ -79,6 +79,8 @@ _SIGS = {
     "ds4f_gpu_mlx4_matvec": ([_vp, _vp, _vp, _i, _i, _vp, _vp], _i),
     "ds4f_gpu_mlx4_batch": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i], _i),
     "ds4f_hip_mlx4_matvec_async": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+    "ds4f_gpu_trunk_roles": ([_vp, _i, _vp], _i),
+    "ds4f_gpu_attn_weights_trunk": ([_i, _vp, _i, _vp], _i),
 }
 
 _lib = None

@@ -265,6 +265,49 @@ typedef struct Ds4fGpuLayerW {
  * every layer (the projections' cols).  A second call replaces the copy. */
 int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w);
 
+/* One tensor of a layer's entry in the engine's packed trunk, laid out as
+ * the engine's own Ds4fTrunkTensor (include/ds4f/moe.h:49-56) so the engine
+ * passes its parsed list (tl->t + tl->t_off[L]) unchanged: checkpoint name,
+ * dtype code (0 = F32, 4 = BF16, 5 = U32, as src/moe.c:36-42), dims, rank,
+ * byte offset in the layer's payload (its bytes of trunk.bin), size. */
+typedef struct Ds4fGpuTrunkTensor {
+    char name[96];
+    int  dtype;
+    long dims[4];
+    int  rank;
+    long off;
+    long nbytes;
+} Ds4fGpuTrunkTensor;
+
+/* Indices into a layer's tensor list of the roles the attention steps read
+ * (-1: absent); an MLX projection is [weight, scales, biases]. */
+typedef struct Ds4fGpuTrunkRoles {
+    int in_norm;
+    int q[3], k[3], v[3], o[3];
+    int q_norm, k_norm;
+    int conv, A_log, dt_bias;
+    int qkv[3], z[3], a[3], b[3], out[3];
+    int norm;
+} Ds4fGpuTrunkRoles;
+
+/* Resolve the roles of one layer's tensor list by the reference's name
+ * suffixes, first match winning (ds4f_trunk_layout_load, src/moe.c:372-373,
+ * :425-490).  Returns the layer's kind by the dispatch of
+ * ds4f_attn_qwen_step (src/attn_qwen.c:1259-1263): DS4F_LAYER_GQA when a
+ * q_proj weight is present, DS4F_LAYER_LINEAR when conv1d or in_proj_qkv is,
+ * DS4F_LAYER_NONE otherwise; -1 on bad arguments.  Needs no GPU. */
+int ds4f_gpu_trunk_roles(const Ds4fGpuTrunkTensor *t, int n, Ds4fGpuTrunkRoles *roles);
+
+/* ds4f_gpu_attn_weights from the trunk: layer L's tensor list t[0..n) and
+ * its payload tr (the layer's bytes of trunk.bin, as the engine streams
+ * them, src/trunk.c).  MLX weights are U32 [rows, cols / 8] (decoded cols
+ * dims[1] * 8, src/attn_qwen.c:103-105) with BF16 scales / biases; norms,
+ * conv1d and dt_bias BF16; A_log F32.  A list with no attention roles
+ * uploads nothing and returns 0; a missing role or a dtype other than
+ * these returns -1 with the reason in ds4f_gpu_last_error. */
+int ds4f_gpu_attn_weights_trunk(int L, const Ds4fGpuTrunkTensor *t, int n,
+                                const uint8_t *tr);
+
 /* One decode token of layer L on the residual stream, the whole of
  * ds4f_attn_qwen_step for that layer (src/attn_qwen.c:1255-1264 ->
  * gqa_step :87-225 or linear_step :837-968): xin = input_layernorm(state),

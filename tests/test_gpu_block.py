@@ -44,9 +44,10 @@ def _err(got, ref):
     return mx, rr
 
 
-def _stack(kinds, n_past, token0, max_tokens, seed=0):
+def _stack(kinds, n_past, token0, max_tokens, seed=0, upload=True):
     """A bound stack with synthetic caches / states / conv rings and layer
-    weights on both sides; returns (plugin, oracle state per layer, weights)."""
+    weights on both sides (upload=False: the device gets no weights);
+    returns (plugin, oracle state per layer, weights)."""
     cache = KvCache(len(kinds), max_tokens)
     ref = {}
     ws = {}
@@ -64,8 +65,9 @@ def _stack(kinds, n_past, token0, max_tokens, seed=0):
             ref[L] = (cache.conv[L].copy(), cache.lin[L].copy())
             ws[L] = W.lin_layer_weights(LG, HID, seed, L)
     ga = GpuAttention(kinds, max_tokens, cache, n_kv_tokens=n_past)
-    for L, w in ws.items():
-        ga.set_layer_weights(L, w)
+    if upload:
+        for L, w in ws.items():
+            ga.set_layer_weights(L, w)
     return ga, ref, ws
 
 
@@ -454,3 +456,66 @@ def test_chunk_fp16_range_falls_back(kind):
         _say(f"  state rel {srel:.3e}")
         assert np.array_equal(dev_S, step_S)
         assert srel <= 1e-4
+
+
+def test_layer_steps_from_trunk(tmp_path):
+    """Weights from the engine's packed trunk: a lin-lin-lin-GQA stack's
+    layers written in the on-disk layout of tools/build-trunk-mlx.py, read
+    back into per-layer tensor lists (the engine's Ds4fTrunkTensor) and
+    payloads, and uploaded with ds4f_gpu_attn_weights_trunk.  Three decode
+    tokens through the four layers match the oracle's layer steps on the
+    same weights, and bit for bit the same steps with the weights given to
+    ds4f_gpu_attn_weights directly.  A layer list missing a role is refused
+    with the role named."""
+    import ctypes
+
+    from ds4f_hip import trunk as T
+
+    kinds = [1, 1, 1, 2]
+    n_past = 60
+    ga, ref, ws = _stack(kinds, n_past, n_past, 256, seed=4)      # direct registration
+    ga.close()
+    T.write_trunk(str(tmp_path), {L: T.layer_entries(L, w) for L, w in ws.items()})
+    tr = T.read_trunk(str(tmp_path))
+
+    def steps(ga_):
+        out = []
+        for s in range(3):
+            st = W.hidden_state(HID, 4, 400 + s)
+            for Lr in range(len(kinds)):
+                st = ga_.attn_step(Lr, n_past + s, st)
+            out.append(st)
+        return out
+
+    ga_d, _, _ = _stack(kinds, n_past, n_past, 256, seed=4)
+    try:
+        direct = steps(ga_d)
+    finally:
+        ga_d.close()
+    ga_t, ref, _ = _stack(kinds, n_past, n_past, 256, seed=4, upload=False)
+    try:
+        with pytest.raises(RuntimeError, match="no weights"):
+            ga_t.attn_step(0, n_past, W.hidden_state(HID, 4, 400))
+        for Lr in range(len(kinds)):
+            tens, payload = tr[Lr]
+            rc = ga_t.lib.ds4f_gpu_attn_weights_trunk(Lr, ctypes.cast(tens, ctypes.c_void_p),
+                                                      len(tens), payload.ctypes.data)
+            assert rc == 0, ga_t.lib.ds4f_gpu_last_error()
+        got = steps(ga_t)
+        for s in range(3):
+            st_o = W.hidden_state(HID, 4, 400 + s)
+            for Lr, k in enumerate(kinds):
+                st_o = _oracle_layer(k, ref[Lr], ws[Lr], n_past + s, st_o)
+            mx, rr = _err(got[s], st_o)
+            _say(f"trunk-loaded stack token {n_past + s}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            assert mx <= ATOL
+            assert np.array_equal(got[s], direct[s])
+        # a layer without its k_norm: refused, the role named
+        tens, payload = tr[3]
+        keep = [t for t in tens if not t.name.decode().endswith("k_norm.weight")]
+        short = (T.TrunkTensor * len(keep))(*keep)
+        assert ga_t.lib.ds4f_gpu_attn_weights_trunk(3, ctypes.cast(short, ctypes.c_void_p),
+                                                    len(keep), payload.ctypes.data) == -1
+        assert b"k_norm" in ga_t.lib.ds4f_gpu_last_error()
+    finally:
+        ga_t.close()
