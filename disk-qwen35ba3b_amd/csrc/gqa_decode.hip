@@ -23,7 +23,7 @@
  * the reference does with its fp32 cache) by the last chunk's workgroup,
  * which also writes the bf16 cache row.
  * Kernel 2 (merge): rescales and sums the P partials of each q head and
- * applies the gate.
+ * applies the gate, one wave per (head, 16 dims) with wave reductions only.
  *
  * Every global input of the prologue is loaded up front so the workgroup
  * pays one memory round trip before its main loop, not one per element.
@@ -317,57 +317,67 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     }
 }
 
-/* merge: grid (heads, D/16), 256 threads = 16 chunk groups x 16 dims.  All
- * partial loads of a thread (up to MAX_CHUNKS/16, fully unrolled) and the
- * chunk maxima / sums are issued together: one memory round trip. */
-constexpr int MG = 16;                          /* chunk groups */
-constexpr int MPER = MAX_CHUNKS / MG;           /* chunks per thread, at most */
-__global__ __launch_bounds__(256) void gqa_merge_kernel(Q35GqaDecode p) {
-    const int h = blockIdx.x, g = h / G, hh = h % G;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+/* merge: one wave per (q head, 16 output dims), grid (heads, D/16).  Lane l
+ * takes the chunks l, l + 64, ... (at most MAX_CHUNKS / 64 a lane) and loads
+ * their (max, sum) and 16 output dims in one memory round trip; the maximum,
+ * the weighted sum and the 16 dim totals are wave reductions on DPP lanes,
+ * with no LDS and no barrier. */
+constexpr int MCH = MAX_CHUNKS / 64;            /* chunks a lane, at most */
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, q35_dpp<0xB1>(v));
+    v = fmaxf(v, q35_dpp<0x4E>(v));
+    v = fmaxf(v, q35_dpp<0x141>(v));
+    v = fmaxf(v, q35_dpp<0x140>(v));
+    return fmaxf(fmaxf(q35_readlane(v, 0), q35_readlane(v, 16)),
+                 fmaxf(q35_readlane(v, 32), q35_readlane(v, 48)));
+}
+__global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
+    const int h = blockIdx.x, g = h / G, hh = h % G, d0 = 16 * blockIdx.y;
+    const int lane = threadIdx.x;
     const int P = p.n_chunks;
-    __shared__ float sred[MG][16];
-    __shared__ float swave[2][4];
-    const int cg = t >> 4, dd = t & 15, d = blockIdx.y * 16 + dd;
-    const float *pml = p.part_ml + ((size_t)g * P * G + hh) * 2;
-    const float *po = p.part_o + ((size_t)g * P * G + hh) * D + d;
+    float mc[MCH], lc[MCH];
+    float4 oc[MCH][4];
+#pragma unroll
+    for (int j = 0; j < MCH; j++) {
+        const int c = lane + 64 * j;
+        const bool valid = c < P;
+        const size_t row = (size_t)(g * P + (valid ? c : 0)) * G + hh;
+        const float2 ml = valid ? *reinterpret_cast<const float2 *>(p.part_ml + row * 2)
+                                : make_float2(-INFINITY, 0.0f);
+        mc[j] = ml.x;
+        lc[j] = ml.y;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            oc[j][q] = valid ? *reinterpret_cast<const float4 *>(p.part_o + row * D + d0 + 4 * q)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float gate = lane < 16 ? p.q_gate[(size_t)h * 2 * D + D + d0 + lane] : 0.0f;
 
-    float mc = -INFINITY, lc = 0.0f;
-    if (t < P) {
-        mc = pml[(size_t)t * G * 2];
-        lc = pml[(size_t)t * G * 2 + 1];
+    float M = mc[0];
+#pragma unroll
+    for (int j = 1; j < MCH; j++) M = fmaxf(M, mc[j]);
+    M = wave_max(M);
+    float wgt[MCH], ls = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MCH; j++) {
+        wgt[j] = (mc[j] == -INFINITY) ? 0.0f : q35_exp(mc[j] - M);
+        ls = fmaf(lc[j], wgt[j], ls);
     }
-    float ov[MPER], mv[MPER];
+    const float L = q35_wave_sum(ls);
+    float mine = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MPER; j++) {
-        const int c = cg + MG * j;
-        ov[j] = (c < P) ? po[(size_t)c * G * D] : 0.0f;
-        mv[j] = (c < P) ? pml[(size_t)c * G * 2] : -INFINITY;
+    for (int d = 0; d < 16; d++) {
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MCH; j++) {
+            const float4 o4 = oc[j][d >> 2];
+            const float od = (d & 3) == 0 ? o4.x : (d & 3) == 1 ? o4.y : (d & 3) == 2 ? o4.z : o4.w;
+            v = fmaf(od, wgt[j], v);
+        }
+        v = q35_wave_sum(v);
+        mine = lane == d ? v : mine;
     }
-    const float gate = p.q_gate[(size_t)h * 2 * D + D + d];
-
-    float M = mc;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    if (lane == 0) swave[0][w] = M;
-    q35_lds_barrier();
-    M = fmaxf(fmaxf(swave[0][0], swave[0][1]), fmaxf(swave[0][2], swave[0][3]));
-    const float f = (mc != -INFINITY) ? q35_exp(mc - M) : 0.0f;
-    const float L0 = q35_wave_sum(lc * f);
-    if (lane == 0) swave[1][w] = L0;
-    float o = 0.0f;
-#pragma unroll
-    for (int j = 0; j < MPER; j++)
-        if (mv[j] != -INFINITY) o += ov[j] * q35_exp(mv[j] - M);
-    sred[cg][dd] = o;
-    q35_lds_barrier();
-    if (cg == 0) {
-        const float L = (swave[1][0] + swave[1][1]) + (swave[1][2] + swave[1][3]);
-        float ot = 0.0f;
-#pragma unroll
-        for (int k = 0; k < MG; k++) ot += sred[k][dd];
-        p.attn_out[(size_t)h * D + d] = (ot / L) * q35_sigmoid(gate);
-    }
+    if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = (mine / L) * q35_sigmoid(gate);
 }
 
 }  // namespace
@@ -394,6 +404,6 @@ extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) 
                        dim3(NT), 0, stream, *p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 16), dim3(256), 0, stream, *p);
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 16), dim3(64), 0, stream, *p);
     return hipGetLastError();
 }
