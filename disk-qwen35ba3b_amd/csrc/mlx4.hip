@@ -132,11 +132,6 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
                 q.bi[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(br, 2 * gg, 0, 0);
             }
     };
-    /* the first rows' weights go out before x is read: the weight stream
-     * and the x / norm prologue share one memory round trip */
-    Rows cur;
-    load_rows(RP * wave, cur);
-
     /* x, and with x_norm its RMSNorm, once per workgroup: thread t holds
      * float4s t, t + NT, ... of x (range-checked loads: columns past C read
      * zero), the square sum in double meets over the workgroup, r = sqrtf(mean
@@ -168,8 +163,14 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
             nw[q][1] = n2[1];
         }
     }
-    /* every prologue load is issued before the first wait: the scheduler
-     * would otherwise sink the weight loads below the norm's reduction */
+    /* the first rows' weights go out right after x: loads return in issue
+     * order, so the prologue below waits for x alone and runs while the
+     * weights stream in (issued first, they would hold x's wait until the
+     * wave's whole weight tile had arrived).  The scheduler barriers keep
+     * that order and keep the weight loads above the norm's reduction. */
+    __builtin_amdgcn_sched_barrier(0);
+    Rows cur;
+    load_rows(RP * wave, cur);
     __builtin_amdgcn_sched_barrier(0);
     if (NORM) {
         double ss = 0.0;
