@@ -1065,9 +1065,10 @@ def run_block_prefill(args) -> int:
     tflops = flops / (ev_sec / K) / 1e12
     roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "whole pass: 40 x (xprep + mlx4 dequant GEMM + prefill core + xprep + "
-                          "mlx4 dequant GEMM); peak is the fp16 one, the delta-rule core runs "
-                          "on fp32 MFMA",
+                "kernel": "whole pass: 40 x (xprep + mlx4 dequant GEMM + prefill core + output "
+                          "GEMM), the 10 GQA layers with an xprep before their output GEMM, the "
+                          "30 delta-rule layers with the gated norm writing its X operand; peak "
+                          "is the fp16 one, the delta-rule core runs on fp32 MFMA",
                 "launches": K, "us_per_launch": round(ev_sec / K * 1e6, 2),
                 "flops_per_launch": flops, "gemm_flops": gemm_flops, "gqa_flops": gqa_flops,
                 "lin_flops": lin_flops}
