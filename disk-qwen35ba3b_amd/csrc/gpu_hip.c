@@ -438,9 +438,9 @@ int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate, const 
     if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
     if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;   /* src/attn_qwen.c:256 */
     if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
-    size_t qb, kb, vb;
-    q35_gqa_prefill_ws_bytes(t0, B, P.g.n_kv_heads, &qb, &kb, &vb);
-    if (ensure_ws(qb + kb + vb) != 0) return -1;
+    size_t kb, vb;
+    q35_gqa_prefill_ws_bytes(t0, B, P.g.n_kv_heads, &kb, &vb);
+    if (ensure_ws(kb + vb) != 0) return -1;
     Q35GqaPrefill p;
     memset(&p, 0, sizeof p);
     p.q_gate = q_gate;
@@ -451,9 +451,8 @@ int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate, const 
     p.rope = P.d_rope;
     p.kt = layer_k(P.slot[L]);
     p.vt = layer_v(P.slot[L]);
-    p.qw = (uint16_t *)P.d_ws;
-    p.kw = (uint16_t *)((char *)P.d_ws + qb);
-    p.vw = (uint16_t *)((char *)P.d_ws + qb + kb);
+    p.kw = (uint16_t *)P.d_ws;
+    p.vw = (uint16_t *)((char *)P.d_ws + kb);
     p.attn_out = attn_out;
     p.k_post = k_post;
     p.t0 = t0;

@@ -5,11 +5,12 @@
  * Replaces the serial gqa_body loop of ds4f_attn_gqa_chunk
  * (src/attn_qwen.c:1222-1231): the results equal B decode steps in order.
  *
- * 1. prep:   one workgroup per new token: q_norm / k_norm + half-split RoPE
- *            (src/attn_qwen.c:287-326), the bf16 cache rows of k, and fp16
- *            copies of q and k in MFMA-ready workspaces; vprep: v into the
- *            fp16 workspace and the bf16 cache, transposed through LDS per
- *            32-key block.
+ * 1. prep:   one wave per new token: k_norm + half-split RoPE of the kv heads
+ *            (src/attn_qwen.c:287-326), their bf16 cache rows and fp16
+ *            copies in the MFMA-ready key workspace; vprep: v into the fp16
+ *            workspace and the bf16 cache, transposed through LDS per
+ *            32-key block.  q is normalised and rotated by the attention
+ *            kernel as it loads its q block (below).
  * 2. prefix: cache rows of positions before t0 (earlier chunks) into the
  *            fp16 key / value workspaces; zero padding rows (only launched
  *            when there are such rows).
@@ -89,57 +90,34 @@ __device__ __forceinline__ size_t vw_index(int g, int kbt, int kb, int d, int sl
 }
 
 __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
-    const int b = blockIdx.x, pos = p.t0 + b;
-    const int t = threadIdx.x, w = t >> 6, lane = t & 63, d0 = lane * 4;
+    const int b = 4 * blockIdx.x + (threadIdx.x >> 6), pos = p.t0 + b;
+    const int lane = threadIdx.x & 63, d0 = lane * 4;
+    if (b >= p.B) return;                   /* wave-uniform; no barrier follows */
     const float *rope = p.rope + (size_t)pos * RD;
-
-    float4 xq[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; hh++)
-        xq[hh] = *reinterpret_cast<const float4 *>(p.q_gate + ((size_t)b * p.heads + 4 * w + hh) * 2 * D + d0);
-    const uint2 wq = *reinterpret_cast<const uint2 *>(p.qn_w + d0);
     float4 rc = make_float4(1.f, 1.f, 1.f, 1.f), rs = make_float4(0.f, 0.f, 0.f, 0.f);
     if (lane < RD / 4) {
         rc = *reinterpret_cast<const float4 *>(rope + (d0 & (RD / 2 - 1)));
         rs = *reinterpret_cast<const float4 *>(rope + RD / 2 + (d0 & (RD / 2 - 1)));
     }
+    const uint2 wk = *reinterpret_cast<const uint2 *>(p.kn_w + d0);
     float4 xk[2];
-    uint2 wk = make_uint2(0, 0);
-    if (w == 0) {
-        wk = *reinterpret_cast<const uint2 *>(p.kn_w + d0);
 #pragma unroll
-        for (int g = 0; g < 2; g++)
-            xk[g] = *reinterpret_cast<const float4 *>(p.k_in + ((size_t)b * p.kv_heads + g) * D + d0);
-    }
-
-    const int qb = b >> 4, qp = b & 15;
+    for (int g = 0; g < 2; g++)
+        xk[g] = *reinterpret_cast<const float4 *>(p.k_in + ((size_t)b * p.kv_heads + g) * D + d0);
 #pragma unroll
-    for (int hh = 0; hh < 4; hh++) {
-        const int head = 4 * w + hh, g = head / G, hl = head % G;
-        const float4 y = q35_norm_rope_head(xq[hh], wq, rc, rs, lane);
+    for (int g = 0; g < 2; g++) {
+        const float4 y = q35_norm_rope_head(xk[g], wk, rc, rs, lane);
         q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(y.x) || q35_f16_over(y.y) ||
                                                         q35_f16_over(y.z) || q35_f16_over(y.w));
-        uint16_t *dst = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + qp) * D + d0;
-        const uint2 pk = make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
-                                    (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
-        *reinterpret_cast<uint2 *>(dst) = pk;
-    }
-    if (w == 0) {
+        if (p.k_post)
+            *reinterpret_cast<float4 *>(p.k_post + ((size_t)b * p.kv_heads + g) * D + d0) = y;
+        uint16_t *dst = p.kw + kw_index(g, p.kbt, pos, d0);
+        *reinterpret_cast<uint2 *>(dst) =
+            make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
+                       (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
+        const float yy[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
-        for (int g = 0; g < 2; g++) {
-            const float4 y = q35_norm_rope_head(xk[g], wk, rc, rs, lane);
-            q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(y.x) || q35_f16_over(y.y) ||
-                                                            q35_f16_over(y.z) || q35_f16_over(y.w));
-            if (p.k_post)
-                *reinterpret_cast<float4 *>(p.k_post + ((size_t)b * p.kv_heads + g) * D + d0) = y;
-            uint16_t *dst = p.kw + kw_index(g, p.kbt, pos, d0);
-            *reinterpret_cast<uint2 *>(dst) =
-                make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
-                           (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
-            const float yy[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) p.kt[q35_k_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(yy[e]);
-        }
+        for (int e = 0; e < 4; e++) p.kt[q35_k_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(yy[e]);
     }
 }
 
@@ -207,19 +185,6 @@ __global__ void prefix_kernel(Q35GqaPrefill p, int n_rows) {
     p.vw[vw_index(g, p.kbt, pos >> 5, d, v_slot(pos & 31))] = f16_bits(vf);
 }
 
-/* q workspace rows [B, 16*nqb) of the last block: zeros */
-__global__ void qpad_kernel(Q35GqaPrefill p, int n_pad) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)p.kv_heads * G * n_pad * D) return;
-    const int d = (int)(i % D);
-    const int64_t row = i / D;
-    const int qpos = p.B + (int)(row % n_pad);
-    const int hl = (int)((row / n_pad) % G), g = (int)(row / ((int64_t)n_pad * G));
-    p.qw[((((size_t)g * p.nqb + (qpos >> 4)) * G + hl) * 16 + (qpos & 15)) * D + d] = 0;
-}
-
-
-
 /* LDS: per group, two stages of one 32-key block, each the K tile (16 KB,
  * granule-major as in the workspace) followed by the V tile (16 KB, rows
  * swizzled as in the workspace).  A stage is a verbatim copy of the two
@@ -282,13 +247,90 @@ __device__ __forceinline__ void store_rows(const Q35GqaPrefill &p, int g, int qb
 }
 
 /* Q^T of q block qb as the B operand for the wave's 32 columns, all 16
- * k-steps */
+ * k-steps, straight from the fp32 q rows: lane (col, h) holds dims
+ * 16 ks + 8 h .. +7 of column col (head 2 wg + col / 16, position col % 16
+ * of the block), so a head's 256 dims are split between lanes l and l ^ 32
+ * and the half-split RoPE pairs (d, d + 32), d < 32, sit in k-steps ks and
+ * ks + 2 of one lane.  q_norm as src/attn_qwen.c:287-300 (the square sum in
+ * double, eps on the mean) and the RoPE as :302-326, in the operation order
+ * of q35_norm_rope_head, except that x / r is x times 1 / r: the operand is
+ * rounded to fp16 next (2^-11 relative), which hides the last-place
+ * difference, and 128 IEEE divisions a lane would sit on the attention
+ * kernel's critical path.  Two passes over the row (the sum, then the
+ * normalised values), the second from L2.  Rows past the batch are
+ * range-checked loads that read zero. */
 __device__ __forceinline__ void load_q(const Q35GqaPrefill &p, int g, int qb, int hl, int col, int h,
                                        f16x8_t (&qop)[16]) {
-    const uint16_t *qrow = p.qw + ((((size_t)g * p.nqb + qb) * G + hl) * 16 + (col & 15)) * D;
+#pragma clang fp contract(off)
+    const int b = 16 * qb + (col & 15);
+    const bool live = b < p.B;
+    const int head = g * G + hl;
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<float *>(p.q_gate)), 0, p.B * p.heads * 2 * D * 4, Q35_BUF_DW3);
+    /* a dead row's offset lies past the view for every k-step */
+    const uint32_t off = live ? (uint32_t)((b * p.heads + head) * 2 * D + 8 * h) * 4 : 0x80000000u;
+    auto ld8 = [&](int ks, float (&x)[8]) {
+        const u32x4_t a0 = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(off + 64 * ks), 0, 0);
+        const u32x4_t a1 = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(off + 64 * ks + 16), 0, 0);
 #pragma unroll
-    for (int ks = 0; ks < 16; ks++)
-        qop[ks] = *reinterpret_cast<const f16x8_t *>(qrow + 16 * ks + 8 * h);
+        for (int e = 0; e < 4; e++) {
+            x[e] = __uint_as_float(a0[e]);
+            x[4 + e] = __uint_as_float(a1[e]);
+        }
+    };
+    double ss = 0.0;
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) {
+        float x[8];
+        ld8(ks, x);
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += (double)x[e] * x[e];
+    }
+    ss += __shfl_xor(ss, 32);
+    const float r = sqrtf((float)(ss / (double)D) + 1e-6f), ri = 1.0f / r;
+    const float *rope = p.rope + (size_t)(p.t0 + (live ? b : 0)) * RD;
+    float y[2][8];                  /* dims of k-steps 0, 1 until their RoPE partners come */
+    bool over = false;
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) {
+        float x[8];
+        ld8(ks, x);
+        const uint2 w0 = *reinterpret_cast<const uint2 *>(p.qn_w + 16 * ks + 8 * h);
+        const uint2 w1 = *reinterpret_cast<const uint2 *>(p.qn_w + 16 * ks + 8 * h + 4);
+        const uint32_t wd[4] = {w0.x, w0.y, w1.x, w1.y};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = x[e] * ri * q35_bf2f((uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
+        if (ks < 2) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) y[ks][e] = v[e];
+        } else if (ks < 4) {
+            /* RoPE of the pairs (ks - 2, ks), rotary index 16 (ks - 2) + 8 h + e */
+            const float *cs = rope + 16 * (ks - 2) + 8 * h;
+            const float4 c0 = *reinterpret_cast<const float4 *>(cs);
+            const float4 c1 = *reinterpret_cast<const float4 *>(cs + 4);
+            const float4 s0 = *reinterpret_cast<const float4 *>(cs + RD / 2);
+            const float4 s1 = *reinterpret_cast<const float4 *>(cs + RD / 2 + 4);
+            const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v0 = y[ks - 2][e], v1 = v[e];
+                const float a0 = v0 * cc[e] - v1 * sn[e];      /* x0*c - x1*s */
+                const float a1 = v0 * sn[e] + v1 * cc[e];      /* x0*s + x1*c */
+                qop[ks - 2][e] = (_Float16)a0;
+                qop[ks][e] = (_Float16)a1;
+                over = over || q35_f16_over(a0) || q35_f16_over(a1);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                qop[ks][e] = (_Float16)v[e];
+                over = over || q35_f16_over(v[e]);
+            }
+        }
+    }
+    q35_f16_guard(p.status, Q35_STATUS_GQA_F16, over);
 }
 
 /* Causal work per q block grows with its position.  Workgroup x serves a
@@ -534,20 +576,20 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
 
 }  // namespace
 
-extern "C" void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *qw, size_t *kw,
-                                         size_t *vw) {
-    const size_t nqb = (size_t)(B + 15) / 16, kbt = (size_t)(t0 + B + 31) / 32;
-    *qw = (size_t)kv_heads * nqb * G * 16 * D * 2;
+extern "C" void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *kw, size_t *vw) {
+    const size_t kbt = (size_t)(t0 + B + 31) / 32;
     *kw = (size_t)kv_heads * kbt * 32 * D * 2;
     *vw = *kw;
 }
 
 extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stream) {
     Q35GqaPrefill p = *pin;
-    if (p.heads != p.kv_heads * G || p.kv_heads != 2 || p.B < 1 || p.t0 < 0) return hipErrorInvalidValue;
+    if (p.heads != p.kv_heads * G || p.kv_heads != 2 || p.B < 1 || p.t0 < 0 ||
+        (int64_t)p.B * p.heads * 2 * D * 4 >= ((int64_t)1 << 31))
+        return hipErrorInvalidValue;
     p.nqb = (p.B + 15) / 16;
     p.kbt = (p.t0 + p.B + 31) / 32;
-    hipLaunchKernelGGL(prep_kernel, dim3(p.B), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(prep_kernel, dim3((p.B + 3) / 4), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     {
@@ -561,14 +603,6 @@ extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stre
         const int64_t n = (int64_t)p.kv_heads * n_rows * D;
         hipLaunchKernelGGL(prefix_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
                            n_rows);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
-    const int n_pad = p.nqb * 16 - p.B;
-    if (n_pad > 0) {
-        const int64_t n = (int64_t)p.kv_heads * G * n_pad * D;
-        hipLaunchKernelGGL(qpad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
-                           n_pad);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -105,25 +105,26 @@ void q35_gqa_split(int n_past, int *chunk, int *n_chunks);
 int q35_gqa_max_chunks(void);
 
 /* ---- GQA prefill: causal flash attention over B new tokens ---- *
- * Workspaces (fp16 bits, filled by the prep kernels):
- *   qw  [KVH][nqb][8 heads][16 pos][D]        nqb = ceil(B/16)
+ * Workspaces (fp16 bits, filled by the prep kernels; q is read from q_gate
+ * by the attention kernel itself):
  *   kw  [KVH][kbt][32 keys][D]                kbt = ceil((t0+B)/32)
  *   vw  [KVH][kbt][D][32 keys, MFMA order]
- * q35_gqa_prefill_ws_bytes() gives the three sizes. */
+ * q35_gqa_prefill_ws_bytes() gives the two sizes.  B * H * 2D floats of
+ * q_gate must stay below 2 GiB (the attention kernel's view of it). */
 typedef struct Q35GqaPrefill {
     const float *q_gate;           /* [B][H][2D] */
     const float *k_in, *v_in;      /* [B][KVH][D] */
     const uint16_t *qn_w, *kn_w;
     const float *rope;             /* table [max_tokens][rd]: cos then sin */
     uint16_t *kt, *vt;             /* this layer's K / V cache tiles */
-    uint16_t *qw, *kw, *vw;        /* fp16 workspaces */
+    uint16_t *kw, *vw;             /* fp16 workspaces */
     float *attn_out;               /* [B][H][D] */
     float *k_post;                 /* optional [B][KVH][D] */
     int t0, B, t_tiles, heads, kv_heads;
     int nqb, kbt;
     int *status;                   /* Q35_STATUS_GQA_F16, or NULL */
 } Q35GqaPrefill;
-void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *qw, size_t *kw, size_t *vw);
+void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *kw, size_t *vw);
 hipError_t q35_gqa_prefill(const Q35GqaPrefill *p, hipStream_t stream);
 
 /* ---- state movement between host row layouts and device layouts ---- */
