@@ -361,7 +361,19 @@ __device__ __forceinline__ void load_q(const Q35GqaPrefill &p, int g, int qb, in
  * tile of tile it (which it reads in the next interval), so no stage part
  * is written in an interval in which its group reads it. */
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kernel(Q35GqaPrefill p) {
-    const int g = blockIdx.y;
+    /* 1-D grid over (pair, kv head).  Workgroups go to the 8 XCDs in turn
+     * (id mod 8); with the pair count a multiple of 4, XCDs 0-3 take kv
+     * head 0 and XCDs 4-7 kv head 1, so each XCD's L2 holds one head's K /
+     * V workspaces (4 MB at 4096 tokens) instead of both */
+    const int np = (p.nqb + 1) / 2, L = blockIdx.x;
+    int x, g;
+    if (p.kv_heads == 2 && (np & 3) == 0) {
+        g = (L & 7) >> 2;
+        x = (L >> 3) * 4 + (L & 3);
+    } else {
+        g = L / np;
+        x = L % np;
+    }
     const int t = threadIdx.x, lane = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int grp = w >> 2, wg = w & 3;
@@ -372,7 +384,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
     __shared__ __align__(16) _Float16 smem[4 * STAGE];   /* [group][stage] */
     __shared__ float sml[4][2][64];                      /* group B's m, l */
 
-    const int x = blockIdx.x, qL = p.nqb - 1 - x, qS = x;
+    const int qL = p.nqb - 1 - x, qS = x;
     const bool has_short = qS < qL;
     const int nL = (min(p.t0 + 16 * qL + 16, end) + 31) >> 5;
     const int nS = has_short ? (min(p.t0 + 16 * qS + 16, end) + 31) >> 5 : 0;
@@ -606,6 +618,6 @@ extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stre
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(attn_kernel, dim3((p.nqb + 1) / 2, p.kv_heads), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(attn_kernel, dim3((p.nqb + 1) / 2 * p.kv_heads), dim3(512), 0, stream, p);
     return hipGetLastError();
 }
