@@ -354,9 +354,12 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  * issue no global loads inside the loop, so their output stores never make
  * them wait, and the loaders' loads are unconditional raw buffer loads
  * (range-checked: rows past the batch read as zero), so their waits count
- * exactly.  Workgroup n runs head (n & 7) + 8 (n >> 6), block (n >> 3) & 7:
- * the 8 blocks of a head share an XCD (workgroups are dealt round-robin
- * over the 8 XCDs), so the operands they all read stay in one L2. */
+ * exactly.  Workgroups are dealt round-robin over the 8 XCDs (id mod 8):
+ * with 8 | key heads, workgroup n runs key head (n & 7) + 8 (n >> 7), its
+ * value head (n >> 6) & 1 and block (n >> 3) & 7, so the 16 workgroups of a
+ * key head (both value heads, all blocks: they all read its Q and K rows)
+ * share one XCD and its L2; otherwise head (n & 7) + 8 (n >> 6), block
+ * (n >> 3) & 7 (the 8 blocks of a value head on one XCD). */
 constexpr int OS = 20;                 /* LDS row stride of the V tile */
 constexpr int SCAN_THREADS = 512;
 
@@ -476,7 +479,11 @@ __device__ __forceinline__ void r2_store(const StageR2 &st, ScanLds &L, int lt) 
 __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     const int n = blockIdx.x;
     ScanGeo g;
-    g.h = (n & 7) + 8 * (n >> 6);
+    if ((p.k_heads & 7) == 0) {
+        g.h = 2 * ((n & 7) + 8 * (n >> 7)) + ((n >> 6) & 1);
+    } else {
+        g.h = (n & 7) + 8 * (n >> 6);
+    }
     g.jb = (n >> 3) & 7;
     g.kh = g.h >> 1;
     g.VH = p.v_heads;
