@@ -265,10 +265,13 @@ __device__ __forceinline__ void load_q(const Q35GqaPrefill &p, int g, int qb, in
     const int b = 16 * qb + (col & 15);
     const bool live = b < p.B;
     const int head = g * G + hl;
+    /* a view of the block's (at most 16) rows; a dead row's offset lies
+     * past it for every k-step */
+    const int rows = min(16, p.B - 16 * qb);
     const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
-        q35_uniform_ptr(const_cast<float *>(p.q_gate)), 0, p.B * p.heads * 2 * D * 4, Q35_BUF_DW3);
-    /* a dead row's offset lies past the view for every k-step */
-    const uint32_t off = live ? (uint32_t)((b * p.heads + head) * 2 * D + 8 * h) * 4 : 0x80000000u;
+        q35_uniform_ptr(const_cast<float *>(p.q_gate + (size_t)16 * qb * p.heads * 2 * D)), 0,
+        rows * p.heads * 2 * D * 4, Q35_BUF_DW3);
+    const uint32_t off = live ? (uint32_t)(((col & 15) * p.heads + head) * 2 * D + 8 * h) * 4 : 0x80000000u;
     auto ld8 = [&](int ks, float (&x)[8]) {
         const u32x4_t a0 = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(off + 64 * ks), 0, 0);
         const u32x4_t a1 = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(off + 64 * ks + 16), 0, 0);
@@ -596,9 +599,7 @@ extern "C" void q35_gqa_prefill_ws_bytes(int t0, int B, int kv_heads, size_t *kw
 
 extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stream) {
     Q35GqaPrefill p = *pin;
-    if (p.heads != p.kv_heads * G || p.kv_heads != 2 || p.B < 1 || p.t0 < 0 ||
-        (int64_t)p.B * p.heads * 2 * D * 4 >= ((int64_t)1 << 31))
-        return hipErrorInvalidValue;
+    if (p.heads != p.kv_heads * G || p.kv_heads != 2 || p.B < 1 || p.t0 < 0) return hipErrorInvalidValue;
     p.nqb = (p.B + 15) / 16;
     p.kbt = (p.t0 + p.B + 31) / 32;
     hipLaunchKernelGGL(prep_kernel, dim3((p.B + 3) / 4), dim3(256), 0, stream, p);

@@ -109,8 +109,7 @@ int q35_gqa_max_chunks(void);
  * by the attention kernel itself):
  *   kw  [KVH][kbt][32 keys][D]                kbt = ceil((t0+B)/32)
  *   vw  [KVH][kbt][D][32 keys, MFMA order]
- * q35_gqa_prefill_ws_bytes() gives the two sizes.  B * H * 2D floats of
- * q_gate must stay below 2 GiB (the attention kernel's view of it). */
+ * q35_gqa_prefill_ws_bytes() gives the two sizes. */
 typedef struct Q35GqaPrefill {
     const float *q_gate;           /* [B][H][2D] */
     const float *k_in, *v_in;      /* [B][KVH][D] */
