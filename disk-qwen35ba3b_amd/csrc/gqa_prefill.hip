@@ -54,6 +54,12 @@ constexpr float EXP_K = SCALE * 1.4426950408889634f;    /* exp(SCALE x) = 2^(EXP
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+/* compile-time switch of the staging loads an MFMA phase issues */
+template <bool ON>
+struct DmaOn {
+    static constexpr bool value = ON;
+};
+
 __device__ __forceinline__ uint16_t f16_bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
@@ -362,7 +368,8 @@ __device__ __forceinline__ void load_q(const Q35GqaPrefill &p, int g, int qb, in
  * stages per group, issued one interval ahead of use: for group A the K
  * and V tiles of tile it+1; for group B the K tile of tile it+1 and the V
  * tile of tile it (which it reads in the next interval), so no stage part
- * is written in an interval in which its group reads it. */
+ * is written in an interval in which its group reads it.  Group A issues
+ * its loads among its QK MFMAs, group B among its PV MFMAs. */
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kernel(Q35GqaPrefill p) {
     /* 1-D grid over (pair, kv head).  Workgroups go to the 8 XCDs in turn
      * (id mod 8); with the pair count a multiple of 4, XCDs 0-3 take kv
@@ -416,6 +423,30 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
             q35_dma16(part ? vrs : krs, base + j * 1024, dma_lane, so + j * 1024);
         }
     };
+    /* Two stage parts (tiles t0 and t1, both below nL) whose eight loads
+     * are issued between the operand-read batches of an MFMA phase: a
+     * load's issue waits while the CU's address unit is busy with other
+     * waves' loads, and placed there that wait runs under the MFMAs
+     * already issued instead of in front of them.  Load i of the pair is
+     * 1 KB block wg + 4 (i & 3) of part (i < 4 ? 0 : 1). */
+    struct Dma2 {
+        uint32_t base[2], so[2];
+        int part[2];
+    };
+    auto dma2 = [&](int stage0, int part0, int tile0, int stage1, int part1, int tile1) {
+        Dma2 d;
+        d.base[0] = lds0 + (uint32_t)((grp * 2 + stage0) * STAGE + part0 * TILE_HALFS) * 2;
+        d.base[1] = lds0 + (uint32_t)((grp * 2 + stage1) * STAGE + part1 * TILE_HALFS) * 2;
+        d.so[0] = (uint32_t)tile0 * TILE_BYTES;
+        d.so[1] = (uint32_t)tile1 * TILE_BYTES;
+        d.part[0] = part0;
+        d.part[1] = part1;
+        return d;
+    };
+    auto dma_issue = [&](const Dma2 &d, int i) {
+        const int k = i >> 2, j = wg + 4 * (i & 3);
+        q35_dma16(d.part[k] ? vrs : krs, d.base[k] + j * 1024, dma_lane, d.so[k] + j * 1024);
+    };
 
     /* operand read addresses: K granule 2ks + h of key col at
      * (2ks + h) * 32 + col; V row 32dt + col, granule h + 2(u & 1) (swizzled) */
@@ -437,20 +468,32 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
     };
 
     /* S^T = K Q^T: lane holds column col, keys 32kb + 8j + 4h + i' */
-    auto qk = [&](int stage, f32x16_t &s) {
+    auto qk = [&](auto dma_on, const Dma2 &d, int stage, f32x16_t &s) {
         const _Float16 *sb = smem + (grp * 2 + stage) * STAGE;
 #pragma unroll
         for (int i = 0; i < 16; i++) s[i] = 0.0f;
         f16x8_t ka[16];
 #pragma unroll
-        for (int ks = 0; ks < 16; ks++) ka[ks] = *reinterpret_cast<const f16x8_t *>(sb + kbase + 512 * ks);
+        for (int ks = 0; ks < 16; ks++) {
+            ka[ks] = *reinterpret_cast<const f16x8_t *>(sb + kbase + 512 * ks);
+            if constexpr (decltype(dma_on)::value) {
+                if (ks == 7 || ks == 11 || ks == 15) {
+                    dma_issue(d, 2 * (ks >> 2) - 2);
+                    dma_issue(d, 2 * (ks >> 2) - 1);
+                }
+            }
+        }
 #pragma unroll
         for (int ks = 0; ks < 16; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[ks], qop[ks], s, 0, 0, 0);
+        if constexpr (decltype(dma_on)::value) {
+            dma_issue(d, 6);
+            dma_issue(d, 7);
+        }
         sched_reads_ahead<4>();
     };
 
     /* online softmax of tile kb of q block qb, then O^T += V^T P^T */
-    auto softmax_pv = [&](int stage, f32x16_t &s, int kb, int qb) {
+    auto softmax_pv = [&](auto dma_on, const Dma2 &d, int stage, f32x16_t &s, int kb, int qb) {
         /* element i is key 32kb + 8(i/4) + 4h + i%4: causal (key <= qpos) and
          * inside the batch (key < end) as one per-lane bound on the
          * compile-time offset 8(i/4) + i%4, applied only on a tile that
@@ -500,16 +543,28 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
         const _Float16 *sb = smem + (grp * 2 + stage) * STAGE;
         f16x8_t va[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
+        for (int u = 0; u < 16; u++) {
             va[u] = *reinterpret_cast<const f16x8_t *>(sb + ((u & 1) ? vb1 : vb0) + 1024 * (u >> 1));
+            if constexpr (decltype(dma_on)::value) {
+                if (u == 7 || u == 11 || u == 15) {
+                    dma_issue(d, 2 * (u >> 2) - 2);
+                    dma_issue(d, 2 * (u >> 2) - 1);
+                }
+            }
+        }
 #pragma unroll
         for (int u = 0; u < 16; u++)
             acc[u >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[u], pb[u & 1], acc[u >> 1], 0, 0, 0);
+        if constexpr (decltype(dma_on)::value) {
+            dma_issue(d, 6);
+            dma_issue(d, 7);
+        }
         sched_reads_ahead<4>();
     };
 
     reset();
     f32x16_t s;
+    const Dma2 dnone = dma2(0, 0, 0, 0, 0, 0);
     if (grp == 0) {
         load_q(p, g, qL, hl, col, h, qop);
         stage_part(0, 0, 0);
@@ -517,12 +572,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
         wait_dma();
         q35_lds_barrier();
         for (int it = 0; it < nA; it++) {
-            /* the next tile's K, then its V, each as a burst of four
-             * loads ahead of the phase that follows */
-            if (it + 1 < nA) stage_part((it + 1) & 1, 0, it + 1);
-            qk(it & 1, s);
-            if (it + 1 < nA) stage_part((it + 1) & 1, 1, it + 1);
-            softmax_pv(it & 1, s, it, qL);
+            /* the next tile's K and V, issued among this tile's QK MFMAs;
+             * in the last interval the clamp reloads tile it into the
+             * stage nobody reads again */
+            const int tn = min(it + 1, nA - 1);
+            qk(DmaOn<true>{}, dma2((it + 1) & 1, 0, tn, (it + 1) & 1, 1, tn), it & 1, s);
+            softmax_pv(DmaOn<false>{}, dnone, it & 1, s, it, qL);
             wait_dma();
             q35_lds_barrier();
         }
@@ -534,9 +589,17 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
         wait_dma();
         q35_lds_barrier();
         for (int it = 0; it < nA; it++) {
-            if (it < nB) stage_part(it & 1, 1, tile_b(it));
+            /* (separate conditions: as an if / else-if chain the
+             * compiler spills a kilobyte a lane) */
+            if (it == 0 && nB > 0) stage_part(0, 1, tile_b(0));
+            if (it == 0 && 1 < nB) stage_part(1, 0, tile_b(1));
             if (it >= 1 && it <= nB) {
-                softmax_pv((it - 1) & 1, s, tile_b(it - 1), block_b(it - 1));
+                /* V of tile it and K of tile it + 1, issued among the PV
+                 * MFMAs of tile it - 1; past the last tile the clamp
+                 * reloads it into stage parts nobody reads again */
+                const int tv = tile_b(min(it, nB - 1)), tk = tile_b(min(it + 1, nB - 1));
+                softmax_pv(DmaOn<true>{}, dma2(it & 1, 1, tv, (it + 1) & 1, 0, tk), (it - 1) & 1, s,
+                           tile_b(it - 1), block_b(it - 1));
                 if (it == nS && it < nB) {
                     /* the short block is done: its rows out, the long
                      * block's tail next */
@@ -549,12 +612,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void attn_kern
                     wait_dma();
                 }
             }
-            if (it + 1 < nB) stage_part((it + 1) & 1, 0, tile_b(it + 1));
-            if (it < nB) qk(it & 1, s);
+            if (it < nB) qk(DmaOn<false>{}, dnone, it & 1, s);
             wait_dma();
             q35_lds_barrier();
         }
-        if (nB == nA && nB > 0) softmax_pv((nB - 1) & 1, s, tile_b(nB - 1), block_b(nB - 1));
+        /* after the last barrier the stages become the merge area: no
+         * staging loads here */
+        if (nB == nA && nB > 0)
+            softmax_pv(DmaOn<false>{}, dnone, (nB - 1) & 1, s, tile_b(nB - 1), block_b(nB - 1));
     }
 
     /* group B's partial of the long block -> LDS -> group A; the stages are
