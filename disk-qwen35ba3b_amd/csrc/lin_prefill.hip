@@ -345,136 +345,106 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  * 8 waves in two roles.  Waves 0-3 compute from LDS only: wave w owns rows
  * 16w.. of X and Delta, rows 16(3-w).. of O (so the causal products are
  * balanced: 116 MFMAs a wave), and key rows 32w..32w+31 of the state
- * block.  Waves 4-7 move the operands global -> registers -> LDS:
- *   R1 = Q, the V slice, exp(G), beta   read in phase 1,  refilled in 1b
- *   R2 = T, Pm, exp(G_C - G), exp(G_C)  read in 1b and 2, refilled in 1
- *   K (double-buffered)                 read in 1 and 2,  refilled in 2
- * so each refill runs under other phases' MFMAs; a loader's global loads
- * are issued one step before their data is written.  The compute waves
- * issue no global loads inside the loop, so their output stores never make
- * them wait, and the loaders' loads are unconditional raw buffer loads
- * (range-checked: rows past the batch read as zero), so their waits count
- * exactly.  Workgroups are dealt round-robin over the 8 XCDs (id mod 8):
- * with 8 | key heads, workgroup n runs key head (n & 7) + 8 (n >> 7), its
- * value head (n >> 6) & 1 and block (n >> 3) & 7, so the 16 workgroups of a
- * key head (both value heads, all blocks: they all read its Q and K rows)
- * share one XCD and its L2; otherwise head (n & 7) + 8 (n >> 6), block
- * (n >> 3) & 7 (the 8 blocks of a value head on one XCD). */
-constexpr int OS = 20;                 /* LDS row stride of the V tile */
+ * block.  Waves 4-7 copy the operands global -> LDS with direct-to-LDS
+ * buffer loads (no register staging), each into the tile's LDS image, and
+ * count their own loads (vmcnt) before the barrier that publishes a tile:
+ *   K (double-buffered)          read in 1 and 2, copied for c + 1 in 1 of c
+ *   Q, V, exp(G), beta           read in 1,       copied for c + 1 in 1b of c
+ *   T                            read in 1b,      copied for c + 1 in 2 of c
+ *   Pm, exp(G_C - G), exp(G_C)   read in 2,       copied for c in 1 of c
+ * so every copy has at least two phases to land.  K, Q, T and Pm rows sit
+ * in LDS with 16-byte granule g of row r at granule g ^ (r % 16) (the
+ * copy's lanes fetch the granule their slot holds): the MFMA operand reads
+ * of 16 consecutive rows hit 16 distinct bank groups.  Workgroups are dealt
+ * round-robin over the 8 XCDs (id mod 8): with 8 | key heads, workgroup n
+ * runs key head (n & 7) + 8 (n >> 7), its value head (n >> 6) & 1 and
+ * block (n >> 3) & 7, so the 16 workgroups of a key head (both value
+ * heads, all blocks: they all read its Q and K rows) share one XCD and its
+ * L2; otherwise head (n & 7) + 8 (n >> 6), block (n >> 3) & 7 (the 8 blocks
+ * of a value head on one XCD). */
 constexpr int SCAN_THREADS = 512;
 
 struct ScanLds {
-    float K[2][C * XS];                /* K rows [t][i], chunk c in K[c & 1] */
-    float Q[C * XS];                   /* R1: Q rows [t][i] */
-    float V[C * OS];                   /* R1: V slice [t][j] */
-    float Gq[C], Beta[C];              /* R1 */
-    float T[C * AS];                   /* R2: T [t][s] */
-    float P[C * AS];                   /* R2: Pm [t][s], upper tiles zero */
-    float Gk[C];                       /* R2: exp(G_C - G_s) */
-    float Gc[4];                       /* R2: exp(G_C) */
+    float K[2][C * KD];                /* K rows [t][i], chunk c in K[c & 1] (sw128) */
+    float Q[C * KD];                   /* Q rows [t][i] (sw128) */
+    float V[C * 16];                   /* V slice [t][j] */
+    float T[C * C];                    /* T [t][s] (sw64) */
+    float P[C * C];                    /* Pm [t][s] (sw64); tiles above the diagonal unread */
+    float G1[Q35_LIN_GVEC];            /* the chunk's gate vector, for exp(G) and beta (phase 1) */
+    float G2[Q35_LIN_GVEC];            /* the same, for exp(G_C - G) and exp(G_C) (phase 2) */
     float S[16 * XS];                  /* state block [j][i] */
     float X[16 * AS];                  /* X [j][t] */
     float D[16 * AS];                  /* Delta [j][t] */
 };
+static_assert(Q35_LIN_GVEC == 256, "a gate vector is four 64-float quarters, one per copy wave");
+
+/* float offset of (row r, column k) in a [rows][128] / [rows][64] tile
+ * stored with granule swizzle g ^ (r % 16) */
+__device__ __forceinline__ int sw128(int r, int k) { return r * KD + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
+__device__ __forceinline__ int sw64(int r, int k) { return r * C + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
 
 struct ScanGeo {
     int h, jb, kh, VH, KH, rows;
-};
-
-/* Loader staging, lane lt of the 256 loader lanes.  All operand loads are
- * raw buffer loads over the chunk's own block with 32-bit lane offsets; T
- * and Pm row group u of lane lt sits at byte 4096 u + 16 lt of its block. */
-struct StageR1 {
-    u32x4_t q[8], v, gq, beta;
-};
-struct StageR2 {
-    u32x4_t t[4], pm[4], gk, gc;
-};
-struct StageK {
-    u32x4_t k[8];
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t blk_rsrc(const float *base, size_t n_floats) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, (int)(n_floats * 4), Q35_BUF_DW3);
 }
 
-/* the post rows of chunk c (rows at and past the batch end read as zero) */
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t post_rsrc(const Q35LinPrefill &p, const ScanGeo &g, int c) {
-    const int b0 = c * C, nv = min(C, p.B - b0);
-    return blk_rsrc(p.post + (size_t)b0 * g.rows, (size_t)nv * g.rows);
-}
+/* The copy waves' loads.  dw = 0..3 is the copy wave; each issues its
+ * share of a tile: 1 KB copies dw, dw + 4, ... (lane l -> LDS bytes
+ * 16 l .. of the copy) and a quarter of a gate vector. */
+struct ScanCopy {
+    const float *post, *T, *Pm, *gvec;
+    int B;
+    ScanGeo g;
+    int dw, lane;
+    uint32_t lK, lQ, lV, lT, lP, lG1, lG2;      /* LDS byte addresses (lK: K[0]; K[1] follows) */
 
-__device__ __forceinline__ void r1_load(StageR1 &st, const Q35LinPrefill &p, const ScanGeo &g,
-                                        int c, int lt) {
-    const size_t ch = (size_t)c * g.VH + g.h;
-    const __amdgpu_buffer_rsrc_t qr = post_rsrc(p, g, c);
-    const __amdgpu_buffer_rsrc_t gr = blk_rsrc(p.gvec + ch * Q35_LIN_GVEC, Q35_LIN_GVEC);
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int r = 8 * u + (lt >> 5);
-        st.q[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, (r * g.rows + g.kh * KD + (lt & 31) * 4) * 4, 0, 0);
+    /* 8 copies of a [64][128] row tile (K or Q rows, channels ch0 ..) */
+    /* the post rows of chunk c (rows at and past the batch end read as zero) */
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows(int c) const {
+        const int b0 = c * C, nv = min(C, B - b0);
+        return blk_rsrc(q35_uniform_ptr(post + (size_t)b0 * g.rows), (size_t)nv * g.rows);
     }
-    st.v = __builtin_amdgcn_raw_buffer_load_b128(
-        qr, ((lt >> 2) * g.rows + 2 * g.KH * KD + g.h * VD + 16 * g.jb + (lt & 3) * 4) * 4, 0, 0);
-    st.gq = __builtin_amdgcn_raw_buffer_load_b128(gr, 16 * (lt & 15), 0, 0);
-    st.beta = __builtin_amdgcn_raw_buffer_load_b128(gr, (2 * C + 4 * (lt & 15)) * 4, 0, 0);
-}
-
-__device__ __forceinline__ void r1_store(const StageR1 &st, ScanLds &L, int lt) {
+    __device__ __forceinline__ void rows128(uint32_t lds, int c, int ch0) const {
+        const __amdgpu_buffer_rsrc_t rs = rows(c);
 #pragma unroll
-    for (int u = 0; u < 8; u++)
-        *reinterpret_cast<u32x4_t *>(&L.Q[(8 * u + (lt >> 5)) * XS + (lt & 31) * 4]) = st.q[u];
-    *reinterpret_cast<u32x4_t *>(&L.V[(lt >> 2) * OS + (lt & 3) * 4]) = st.v;
-    /* lanes lt and lt + 16k write the same four values */
-    *reinterpret_cast<u32x4_t *>(&L.Gq[4 * (lt & 15)]) = st.gq;
-    *reinterpret_cast<u32x4_t *>(&L.Beta[4 * (lt & 15)]) = st.beta;
-}
-
-__device__ __forceinline__ void k_load(StageK &st, const Q35LinPrefill &p, const ScanGeo &g, int c,
-                                       int lt) {
-    const __amdgpu_buffer_rsrc_t kr = post_rsrc(p, g, c);
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int r = 8 * u + (lt >> 5);
-        st.k[u] = __builtin_amdgcn_raw_buffer_load_b128(
-            kr, (r * g.rows + (g.KH + g.kh) * KD + (lt & 31) * 4) * 4, 0, 0);
+        for (int i = 0; i < 8; i++) {
+            const int d = dw + 4 * i, r = 2 * d + (lane >> 5), gr = (lane & 31) ^ (r & 15);
+            q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * d),
+                      (uint32_t)((r * g.rows + ch0 + 4 * gr) * 4), 0);
+        }
     }
-}
-
-__device__ __forceinline__ void k_store(const StageK &st, float *Kb, int lt) {
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-        *reinterpret_cast<u32x4_t *>(&Kb[(8 * u + (lt >> 5)) * XS + (lt & 31) * 4]) = st.k[u];
-}
-
-__device__ __forceinline__ void r2_load(StageR2 &st, const Q35LinPrefill &p, const ScanGeo &g,
-                                        int c, int lt) {
-    const size_t ch = (size_t)c * g.VH + g.h;
-    const __amdgpu_buffer_rsrc_t tr = blk_rsrc(p.T + ch * C * C, C * C);
-    const __amdgpu_buffer_rsrc_t pr = blk_rsrc(p.Pm + ch * C * C, C * C);
-    const __amdgpu_buffer_rsrc_t gr = blk_rsrc(p.gvec + ch * Q35_LIN_GVEC, Q35_LIN_GVEC);
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        st.t[u] = __builtin_amdgcn_raw_buffer_load_b128(tr, 16 * lt, 4096 * u, 0);
-        st.pm[u] = __builtin_amdgcn_raw_buffer_load_b128(pr, 16 * lt, 4096 * u, 0);
+    /* K rows of chunk c into K[buf] */
+    __device__ __forceinline__ void k(int c, int buf) const { rows128(lK + buf * C * KD * 4, c, (g.KH + g.kh) * KD); }
+    __device__ __forceinline__ void q(int c) const { rows128(lQ, c, g.kh * KD); }
+    /* one copy of the V slice (16 rows of 16 floats) */
+    __device__ __forceinline__ void v(int c) const {
+        const __amdgpu_buffer_rsrc_t rs = rows(c);
+        const int r = 16 * dw + (lane >> 2);
+        q35_dma16(rs, __builtin_amdgcn_readfirstlane(lV + 1024 * dw),
+                  (uint32_t)((r * g.rows + 2 * g.KH * KD + g.h * VD + 16 * g.jb + 4 * (lane & 3)) * 4), 0);
     }
-    st.gk = __builtin_amdgcn_raw_buffer_load_b128(gr, (C + 4 * (lt & 15)) * 4, 0, 0);
-    st.gc = __builtin_amdgcn_raw_buffer_load_b128(gr, 3 * C * 4, 0, 0);
-}
-
-__device__ __forceinline__ void r2_store(const StageR2 &st, ScanLds &L, int lt) {
-    const int c4 = (lt & 15) * 4;
-    const u32x4_t z = {0u, 0u, 0u, 0u};
+    /* 4 copies of a [64][64] tile of chunk c's T or Pm */
+    __device__ __forceinline__ void tile64(uint32_t lds, const float *base, int c) const {
+        const size_t ch = (size_t)c * g.VH + g.h;
+        const __amdgpu_buffer_rsrc_t rs = blk_rsrc(q35_uniform_ptr(base + ch * C * C), C * C);
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int r = 16 * u + (lt >> 4);
-        *reinterpret_cast<u32x4_t *>(&L.T[r * AS + c4]) = st.t[u];
-        /* the chunk kernel leaves Pm's tiles above the diagonal unwritten */
-        *reinterpret_cast<u32x4_t *>(&L.P[r * AS + c4]) = (c4 >> 4) > u ? z : st.pm[u];
+        for (int i = 0; i < 4; i++) {
+            const int d = dw + 4 * i, r = 4 * d + (lane >> 4), gr = (lane & 15) ^ (r & 15);
+            q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * d), (uint32_t)((r * C + 4 * gr) * 4), 0);
+        }
     }
-    *reinterpret_cast<u32x4_t *>(&L.Gk[4 * (lt & 15)]) = st.gk;   /* lanes lt, lt + 16k: same values */
-    *reinterpret_cast<u32x4_t *>(&L.Gc[0]) = st.gc;               /* all lanes: same value */
-}
+    __device__ __forceinline__ void t(int c) const { tile64(lT, T, c); }
+    __device__ __forceinline__ void pm(int c) const { tile64(lP, Pm, c); }
+    /* a quarter of chunk c's gate vector */
+    __device__ __forceinline__ void gv(uint32_t lds, int c) const {
+        const size_t ch = (size_t)c * g.VH + g.h;
+        const __amdgpu_buffer_rsrc_t rs = blk_rsrc(q35_uniform_ptr(gvec + ch * Q35_LIN_GVEC), Q35_LIN_GVEC);
+        q35_dma4(rs, __builtin_amdgcn_readfirstlane(lds + 256 * dw), (uint32_t)((64 * dw + lane) * 4), 0);
+    }
+};
 
 __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     const int n = blockIdx.x;
@@ -497,41 +467,53 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     float *state = p.state + ((size_t)g.h * VD + 16 * g.jb) * KD;
 
     if (wave >= 4) {
-        /* ---- loader waves ---- */
-        const int lt = t - 256;
-        StageR1 s1;
-        StageR2 s2;
-        StageK sk;
-        r1_load(s1, p, g, 0, lt);
-        k_load(sk, p, g, 0, lt);
-        r2_load(s2, p, g, 0, lt);
-        r1_store(s1, L, lt);
-        k_store(sk, L.K[0], lt);
-        __builtin_amdgcn_sched_barrier(0);
-        r1_load(s1, p, g, min(1, last), lt);
-        k_load(sk, p, g, min(1, last), lt);
+        /* ---- copy waves: loads counted per wave (13 in step 1, 10 in
+         * step 2, 4 in step 3 of every chunk) ---- */
+        ScanCopy cp;
+        cp.post = p.post;
+        cp.T = p.T;
+        cp.Pm = p.Pm;
+        cp.gvec = p.gvec;
+        cp.B = p.B;
+        cp.g = g;
+        cp.dw = wave - 4;
+        cp.lane = t & 63;
+        cp.lK = q35_lds_addr(L.K[0]);
+        cp.lQ = q35_lds_addr(L.Q);
+        cp.lV = q35_lds_addr(L.V);
+        cp.lT = q35_lds_addr(L.T);
+        cp.lP = q35_lds_addr(L.P);
+        cp.lG1 = q35_lds_addr(L.G1);
+        cp.lG2 = q35_lds_addr(L.G2);
+        cp.k(0, 0);
+        cp.q(0);
+        cp.v(0);
+        cp.gv(cp.lG1, 0);
+        cp.t(0);
+        q35_wait_vm<0>();
         q35_lds_barrier();                                   /* B0 */
-        /* the scheduling barriers keep each set's LDS writes ahead of the
-         * loads that refill its registers: issued in the other order, the
-         * loads go to fresh registers that must be copied back before the
-         * loop repeats, which waits for them */
         for (int c = 0; c <= last; c++) {
-            /* phase 1 of c runs: R2 is free */
-            r2_store(s2, L, lt);
-            __builtin_amdgcn_sched_barrier(0);
-            r2_load(s2, p, g, min(c + 1, last), lt);
+            const int c1 = min(c + 1, last);
+            /* step 1 (phase 1 of c): Pm and gates of c, K of c + 1 into the
+             * buffer phase 2 of c - 1 read (on the last chunk, a copy nobody
+             * reads, which keeps the load counts the same) */
+            cp.pm(c);
+            cp.gv(cp.lG2, c);
+            cp.k(c1, (c + 1) & 1);
+            q35_wait_vm<13>();                               /* T of c has landed */
             q35_lds_barrier();                               /* B1(c) */
-            /* phase 1b of c runs: R1 is free */
-            r1_store(s1, L, lt);
-            __builtin_amdgcn_sched_barrier(0);
-            r1_load(s1, p, g, min(c + 2, last), lt);
+            /* step 2 (phase 1b of c): Q, V, gates of c + 1 */
+            cp.q(c1);
+            cp.v(c1);
+            cp.gv(cp.lG1, c1);
+            q35_wait_vm<18>();                               /* Pm and gates of c */
             q35_lds_barrier();                               /* B2(c) */
-            /* phase 2 of c runs: K[(c + 1) & 1] is free */
-            k_store(sk, L.K[(c + 1) & 1], lt);
-            __builtin_amdgcn_sched_barrier(0);
-            k_load(sk, p, g, min(c + 2, last), lt);
+            /* step 3 (phase 2 of c): T of c + 1 */
+            cp.t(c1);
+            q35_wait_vm<4>();                                /* K, Q, V, gates of c + 1 */
             q35_lds_barrier();                               /* B3(c) */
         }
+        q35_wait_vm<0>();
         return;
     }
 
@@ -555,8 +537,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
         for (int blk = 0; blk < 8; blk++) {
             const int k = 16 * blk + 4 * lq;
             const float4 sb = *reinterpret_cast<const float4 *>(&L.S[l16 * XS + k]);
-            const float4 ka = *reinterpret_cast<const float4 *>(&Kc[(rx + l16) * XS + k]);
-            const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[(ro + l16) * XS + k]);
+            const float4 ka = *reinterpret_cast<const float4 *>(&Kc[sw128(rx + l16, k)]);
+            const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[sw128(ro + l16, k)]);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 ak = mfma4(el(ka, e), el(sb, e), ak);
@@ -568,8 +550,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = rx + 4 * lq + i;
-            xr[i] = L.Beta[r] * (L.V[r * OS + l16] - L.Gq[r] * ak[i]);
-            ao[i] = L.Gq[ro + 4 * lq + i] * aq[i];
+            xr[i] = L.G1[2 * C + r] * (L.V[r * 16 + l16] - L.G1[r] * ak[i]);
+            ao[i] = L.G1[ro + 4 * lq + i] * aq[i];
         }
         *reinterpret_cast<float4 *>(&L.X[l16 * AS + rx + 4 * lq]) = make_float4(xr[0], xr[1], xr[2], xr[3]);
         q35_lds_barrier();                                   /* B1(c) */
@@ -579,7 +561,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= w) {       /* w is wave-uniform: a scalar branch */
-                const float4 ta = *reinterpret_cast<const float4 *>(&L.T[(rx + l16) * AS + 16 * blk + 4 * lq]);
+                const float4 ta = *reinterpret_cast<const float4 *>(&L.T[sw64(rx + l16, 16 * blk + 4 * lq)]);
                 const float4 xb = *reinterpret_cast<const float4 *>(&L.X[l16 * AS + 16 * blk + 4 * lq]);
 #pragma unroll
                 for (int e = 0; e < 4; e++) ad = mfma4(el(ta, e), el(xb, e), ad);
@@ -596,7 +578,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= 3 - w) {
-                const float4 pa = *reinterpret_cast<const float4 *>(&L.P[(ro + l16) * AS + 16 * blk + 4 * lq]);
+                const float4 pa = *reinterpret_cast<const float4 *>(&L.P[sw64(ro + l16, 16 * blk + 4 * lq)]);
 #pragma unroll
                 for (int e = 0; e < 4; e++) ao = mfma4(el(pa, e), el(db[blk], e), ao);
             }
@@ -613,13 +595,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
          * and MFMA), B = exp(G_C - G_s) Delta */
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
-            const float4 gk = *reinterpret_cast<const float4 *>(&L.Gk[16 * blk + 4 * lq]);
+            const float4 gk = *reinterpret_cast<const float4 *>(&L.G2[C + 16 * blk + 4 * lq]);
             db[blk].x *= gk.x;
             db[blk].y *= gk.y;
             db[blk].z *= gk.z;
             db[blk].w *= gk.w;
         }
-        const float gc = L.Gc[0];
+        const float gc = L.G2[3 * C];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             const int i0 = 16 * (2 * w + tt);
@@ -630,7 +612,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
             for (int blk = 0; blk < 4; blk++)
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    acc = mfma4(Kc[(16 * blk + 4 * lq + e) * XS + i0 + l16], el(db[blk], e), acc);
+                    acc = mfma4(Kc[sw128(16 * blk + 4 * lq + e, i0 + l16)], el(db[blk], e), acc);
             *reinterpret_cast<float4 *>(sp) = make_float4(acc[0], acc[1], acc[2], acc[3]);
         }
         q35_lds_barrier();                                   /* B3(c) */
