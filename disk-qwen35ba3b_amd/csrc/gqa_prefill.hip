@@ -226,7 +226,8 @@ __device__ __forceinline__ float half_pair_max(float v) {
 /* this wave's direct-to-LDS loads have landed */
 __device__ __forceinline__ void wait_dma() { q35_wait_vm<0>(); }
 
-/* q block qb's output rows of this wave: O / l times sigmoid(gate), fp32 */
+/* q block qb's output rows of this wave: O / l times sigmoid(gate), fp32;
+ * the sigmoid on the hardware exp / reciprocal (q35_sigmoid_fast) */
 __device__ __forceinline__ void store_rows(const Q35GqaPrefill &p, int g, int qb, int hl, int col,
                                            int h, float l_run, const f32x16_t (&acc)[8]) {
     const int end = p.t0 + p.B, qpos = p.t0 + 16 * qb + (col & 15);
@@ -243,10 +244,10 @@ __device__ __forceinline__ void store_rows(const Q35GqaPrefill &p, int g, int qb
             const int d = 32 * dt + 8 * j + 4 * h;
             const float4 gv = *reinterpret_cast<const float4 *>(gate + d);
             float4 o;
-            o.x = acc[dt][4 * j + 0] * inv * q35_sigmoid(gv.x);
-            o.y = acc[dt][4 * j + 1] * inv * q35_sigmoid(gv.y);
-            o.z = acc[dt][4 * j + 2] * inv * q35_sigmoid(gv.z);
-            o.w = acc[dt][4 * j + 3] * inv * q35_sigmoid(gv.w);
+            o.x = acc[dt][4 * j + 0] * inv * q35_sigmoid_fast(gv.x);
+            o.y = acc[dt][4 * j + 1] * inv * q35_sigmoid_fast(gv.y);
+            o.z = acc[dt][4 * j + 2] * inv * q35_sigmoid_fast(gv.z);
+            o.w = acc[dt][4 * j + 3] * inv * q35_sigmoid_fast(gv.w);
             *reinterpret_cast<float4 *>(out + d) = o;
         }
     }

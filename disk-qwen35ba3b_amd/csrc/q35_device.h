@@ -203,6 +203,14 @@ __device__ __forceinline__ float q35_exp(float x) {
 /* sigmoid written as the reference writes it: 1 / (1 + expf(-x)). */
 __device__ __forceinline__ float q35_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+/* The same on the hardware's approximate exp and reciprocal (v_exp_f32 of
+ * -x log2(e), v_rcp_f32: about 1 ulp each; exp(-x) = inf for very negative
+ * x gives rcp(inf) = 0), for the prefill epilogues, whose outputs carry
+ * fp16-operand error orders of magnitude larger. */
+__device__ __forceinline__ float q35_sigmoid_fast(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
 /* splitmix64 finaliser (public algorithm; the same constants as the
  * reference's ds4f_mix64, src/router.c:11-16). */
 __device__ __forceinline__ uint64_t q35_fmix64(uint64_t z) {
