@@ -121,18 +121,21 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
         *reinterpret_cast<uint2 *>(dst) =
             make_uint2((uint32_t)f16_bits(y.x) | ((uint32_t)f16_bits(y.y) << 16),
                        (uint32_t)f16_bits(y.z) | ((uint32_t)f16_bits(y.w) << 16));
-        const float yy[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) p.kt[q35_k_index(g, pos, d0 + e, p.t_tiles)] = q35_f2bf(yy[e]);
+        /* the 4 dims are consecutive in the cache tile (one 8-byte store) */
+        *reinterpret_cast<uint2 *>(p.kt + q35_k_index(g, pos, d0, p.t_tiles)) =
+            make_uint2((uint32_t)q35_f2bf(y.x) | ((uint32_t)q35_f2bf(y.y) << 16),
+                       (uint32_t)q35_f2bf(y.z) | ((uint32_t)q35_f2bf(y.w) << 16));
     }
 }
 
 /* v of the new tokens -> the fp16 value workspace and the bf16 cache,
  * both dim-major ([dim][keys]).  One workgroup per (32-key block, kv head)
- * transposes the block's rows through LDS, so consecutive lanes write
- * consecutive keys of one dim row (64 B of workspace, 32 B of cache) rather
- * than one 2-byte value per row.  Keys outside [t0, t0+B) are left alone:
- * earlier positions belong to the cache, later ones are workspace padding. */
+ * transposes the block's rows through LDS; a lane then stores 8 keys of
+ * one dim row as one 16-byte granule (workspace slots 8i..8i+7, cache
+ * positions 8i..8i+7 of a 16-position tile).  Keys outside [t0, t0+B) are
+ * left alone: earlier positions belong to the cache, later ones are
+ * workspace padding; a granule holding such keys (the block at t0 or at
+ * t0 + B when those are not multiples of 32) is stored key by key. */
 __global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
     const int kb = (p.t0 >> 5) + (int)blockIdx.x, g = blockIdx.y;
     const int t = threadIdx.x;
@@ -153,21 +156,47 @@ __global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
         sv[r][c4 + 3] = v.w;
     }
     q35_lds_barrier();
-    /* workspace: lane (d, slot) of 32 slots a dim row, key = the slot's key */
+    const bool whole = 32 * kb >= p.t0 && 32 * kb + 32 <= p.t0 + p.B;   /* block-uniform */
+    /* workspace: lane (d, granule q of 4 a dim row), slots 8q..8q+7 */
 #pragma unroll
-    for (int u = 0; u < 32; u++) {
-        const int idx = u * 256 + t, d = idx >> 5, slot = idx & 31;
-        const int r = v_key(slot), pos = 32 * kb + r;
-        if (pos >= p.t0 && pos < p.t0 + p.B)
-            p.vw[vw_index(g, p.kbt, kb, d, slot)] = f16_bits(sv[r][d]);
+    for (int u = 0; u < 4; u++) {
+        const int idx = u * 256 + t, d = idx >> 2, q = idx & 3;
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) h[e] = f16_bits(sv[v_key(8 * q + e)][d]);
+        uint16_t *dst = p.vw + vw_index(g, p.kbt, kb, d, 8 * q);
+        if (whole) {
+            *reinterpret_cast<uint4 *>(dst) =
+                make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                           h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int pos = 32 * kb + v_key(8 * q + e);
+                if (pos >= p.t0 && pos < p.t0 + p.B) dst[e] = h[e];
+            }
+        }
     }
-    /* cache: two 16-token tiles, lane (tile, d, token) */
+    /* cache: lane (tile tt, d, half hf), positions 16tt + 8hf .. +7 */
 #pragma unroll
-    for (int u = 0; u < 32; u++) {
-        const int idx = u * 256 + t, tt = idx >> 12, d = (idx >> 4) & (D - 1), r16 = idx & 15;
-        const int r = tt * 16 + r16, pos = 32 * kb + r;
-        if (pos >= p.t0 && pos < p.t0 + p.B)
-            p.vt[q35_v_index(g, pos, d, p.t_tiles)] = q35_f2bf(sv[r][d]);
+    for (int u = 0; u < 4; u++) {
+        const int idx = u * 256 + t, tt = idx >> 9, d = (idx >> 1) & (D - 1), hf = idx & 1;
+        const int r0 = 16 * tt + 8 * hf;
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) h[e] = q35_f2bf(sv[r0 + e][d]);
+        uint16_t *dst = p.vt + q35_v_index(g, 32 * kb + r0, d, p.t_tiles);
+        if (whole) {
+            *reinterpret_cast<uint4 *>(dst) =
+                make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                           h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int pos = 32 * kb + r0 + e;
+                if (pos >= p.t0 && pos < p.t0 + p.B) dst[e] = h[e];
+            }
+        }
     }
 }
 
