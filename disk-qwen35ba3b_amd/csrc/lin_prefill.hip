@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = 16 * tr + 4 * lq + i;
-                const float dec = expf((float)(sG[v][r] - sG[v][s]));
+                const float dec = __expf((float)(sG[v][r] - sG[v][s]));   /* v_exp_f32, ~1 ulp */
                 o[i] = n < 10 ? (s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f)
                               : (s <= r ? dec * res[k][i] : 0.0f);
             }
