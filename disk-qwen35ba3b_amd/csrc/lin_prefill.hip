@@ -63,9 +63,10 @@ __device__ __forceinline__ float el(const float4 &v, int e) {
  * 16 consecutive tokens: the 19 raw rows they tap are loaded once (a
  * sliding window instead of 4 loads per output).  The q / k norm of a
  * head is a half-wave sum.  Against the reference's per-element IEEE
- * divisions, the SiLU uses v_exp_f32 / v_rcp_f32 and the norm one
- * reciprocal per token (each about 1 ulp): the kernel then runs at the
- * HBM rate of its 2 x B x rows x 4 bytes. */
+ * divisions and double square sums, the SiLU uses v_exp_f32 / v_rcp_f32,
+ * the norm one reciprocal per token (each about 1 ulp) and an fp32 square
+ * sum (128 terms, at most 8e-6 relative, about 1e-7 in practice): the
+ * kernel then runs at the HBM rate of its 2 x B x rows x 4 bytes. */
 constexpr int CT = 16;
 __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
     const int bb = blockIdx.y * CT;
@@ -106,9 +107,9 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
         }
         if (normed) {              /* q or k head: RMS norm (src/attn_qwen.c:522-538) */
 #pragma clang fp contract(off)
-            double ss = (double)y[0] * y[0] + (double)y[1] * y[1] + (double)y[2] * y[2] + (double)y[3] * y[3];
+            float ss = y[0] * y[0] + y[1] * y[1] + y[2] * y[2] + y[3] * y[3];
             ss = q35_half_sum(ss);
-            const float r = sqrtf((float)(ss / (double)KD) + 1e-6f), ri = 1.0f / r;
+            const float r = sqrtf(ss * (1.0f / (float)KD) + 1e-6f), ri = 1.0f / r;
 #pragma unroll
             for (int e = 0; e < 4; e++) y[e] = y[e] * ri * scale;
         }
