@@ -35,8 +35,9 @@
  *                unnormalised into out
  *   gnorm_kernel per (token, value head): RMSNormGated of out with z
  *                (src/attn_qwen.c:726-749)
- * All arithmetic is fp32 (MFMA fp32 products are exact, accumulation fp32)
- * except the conv's SiLU and norm reciprocal (hardware exp / rcp, about
+ * All arithmetic is fp32 (MFMA fp32 products are exact, accumulation fp32);
+ * the conv's SiLU and norm reciprocal, the chunk's decay factors and the
+ * gated norm's sigmoid and reciprocal use the hardware exp / rcp (about
  * 1 ulp); the chunk-local cumulative log-decay is summed in double.
  */
 #include "q35_device.h"
@@ -628,7 +629,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 }
 
 /* ---- 5. RMSNormGated per (token, value head), in place on out ----------- *
- * grid (VH / 4, B), wave w -> head 4*blockIdx.x + w, 2 columns a lane. */
+ * grid (VH / 4, B), wave w -> head 4*blockIdx.x + w, 2 columns a lane.
+ * The reference's operation order (src/attn_qwen.c:726-749) with an fp32
+ * square sum, x times 1 / r and the sigmoid on v_exp / v_rcp (about 1 ulp
+ * each; the prefill outputs are checked to 2e-3). */
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 
 __global__ __launch_bounds__(256) void gnorm_kernel(Q35LinPrefill p) {
@@ -638,14 +642,14 @@ __global__ __launch_bounds__(256) void gnorm_kernel(Q35LinPrefill p) {
     const float2 o = *reinterpret_cast<const float2 *>(p.out + off);
     const float2 z = *reinterpret_cast<const float2 *>(p.z + off);
     const uint32_t nw = *reinterpret_cast<const uint32_t *>(p.norm_w + 2 * lane);
-    double ss = (double)o.x * o.x + (double)o.y * o.y;
+    float ss = o.x * o.x + o.y * o.y;
     ss = q35_wave_sum(ss);
     float2 y;
     {
 #pragma clang fp contract(off)
-        const float r = sqrtf((float)(ss / (double)VD) + 1e-6f);
-        y.x = o.x / r * q35_bf2f((uint16_t)(nw & 0xffff)) * (z.x * q35_sigmoid(z.x));
-        y.y = o.y / r * q35_bf2f((uint16_t)(nw >> 16)) * (z.y * q35_sigmoid(z.y));
+        const float r = sqrtf(ss * (1.0f / (float)VD) + 1e-6f), ri = 1.0f / r;
+        y.x = o.x * ri * q35_bf2f((uint16_t)(nw & 0xffff)) * (z.x * q35_sigmoid_fast(z.x));
+        y.y = o.y * ri * q35_bf2f((uint16_t)(nw >> 16)) * (z.y * q35_sigmoid_fast(z.y));
     }
     if (!p.xw) {
         *reinterpret_cast<float2 *>(p.out + off) = y;
