@@ -319,9 +319,9 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
 
 /* merge: one wave per (q head, 16 output dims), grid (heads, D/16).  Lane l
  * takes the chunks l, l + 64, ... (at most MAX_CHUNKS / 64 a lane) and loads
- * their (max, sum) and 16 output dims in one memory round trip; the maximum,
- * the weighted sum and the 16 dim totals are wave reductions on DPP lanes,
- * with no LDS and no barrier. */
+ * their (max, sum) and 16 output dims in one memory round trip; the maximum
+ * and the weighted sum are wave reductions on DPP lanes and the 16 dim
+ * totals one transposing reduction, with no LDS and no barrier. */
 constexpr int MCH = MAX_CHUNKS / 64;            /* chunks a lane, at most */
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, q35_dpp<0xB1>(v));
@@ -364,20 +364,44 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
         ls = fmaf(lc[j], wgt[j], ls);
     }
     const float L = q35_wave_sum(ls);
-    float mine = 0.0f;
+    float v[16];
 #pragma unroll
     for (int d = 0; d < 16; d++) {
-        float v = 0.0f;
+        v[d] = 0.0f;
 #pragma unroll
         for (int j = 0; j < MCH; j++) {
             const float4 o4 = oc[j][d >> 2];
             const float od = (d & 3) == 0 ? o4.x : (d & 3) == 1 ? o4.y : (d & 3) == 2 ? o4.z : o4.w;
-            v = fmaf(od, wgt[j], v);
+            v[d] = fmaf(od, wgt[j], v[d]);
         }
-        v = q35_wave_sum(v);
-        mine = lane == d ? v : mine;
     }
-    if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = (mine / L) * q35_sigmoid(gate);
+    /* the 16 dim totals over the wave as a transposing reduction: in each
+     * 16-lane row, four pairings (lane i with 15 - i, with its mirror in
+     * the 8-lane half, with i ^ 2, with i ^ 1) each flip one bit of i; a
+     * lane keeps the half of its dims whose index bit matches its own and
+     * adds the partner's copy of that half, so lane i ends with its row's
+     * total of dim i; the four rows are then summed across lanes */
+    const int li = lane & 15;
+    float a8[8], a4[4], a2[2];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const bool hi = li & 8;
+        a8[j] = (hi ? v[j + 8] : v[j]) + q35_dpp<0x140>(hi ? v[j] : v[j + 8]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const bool hi = li & 4;
+        a4[j] = (hi ? a8[j + 4] : a8[j]) + q35_dpp<0x141>(hi ? a8[j] : a8[j + 4]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const bool hi = li & 2;
+        a2[j] = (hi ? a4[j + 2] : a4[j]) + q35_dpp<0x4E>(hi ? a4[j] : a4[j + 2]);
+    }
+    float tot = ((li & 1) ? a2[1] : a2[0]) + q35_dpp<0xB1>((li & 1) ? a2[0] : a2[1]);
+    tot += __shfl_xor(tot, 16);
+    tot += __shfl_xor(tot, 32);
+    if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = (tot / L) * q35_sigmoid(gate);
 }
 
 }  // namespace
