@@ -17,8 +17,8 @@
  *           one DPP lane exchange;
  *   values  O^T[16 dim][16 col] += V^T[16 dim][16 pos] * P^T on 16x16x16
  *           bf16 MFMA, P split the same way (hi | lo columns);
- *   online softmax per wave, the 8 waves merged in LDS, one partial
- *   (max, sum, O[8][256]) written per workgroup.
+ *   online softmax per wave, the 8 waves merged in LDS (wave w merges
+ *   head w), one partial (max, sum, O[8][256]) written per workgroup.
  * The new token (position `token`) is attended in fp32 from registers (as
  * the reference does with its fp32 cache) by the last chunk's workgroup,
  * which also writes the bf16 cache row.
@@ -38,7 +38,7 @@ constexpr int NW = 8, NT = 64 * NW;   /* waves per workgroup, threads */
 constexpr int HPW = G / NW;           /* q heads normed per wave in the prologue */
 constexpr int MAX_CHUNKS = 256;
 constexpr int OS = D + 16;            /* sO head stride: head hq starts 16 hq banks on */
-static_assert(NW == 8 && G == 8, "the wave merge maps lane = 8 * head + wave");
+static_assert(NW == G, "wave w merges q head w of the kv head");
 constexpr float SCALE = 0.0625f;      /* 1/sqrtf(256), src/attn_qwen.c:334 */
 struct KTile { bf16x8_t k[8]; };
 struct VTile { s16x4_t v[16]; };
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     __shared__ __align__(16) float sQ[G][D];
     __shared__ bf16x8_t sQb[8 * 64];
     __shared__ __align__(16) float sO[NW][G * OS];
-    __shared__ float sM[NW + 1][G], sL[NW + 1][G], sF[NW + 1][G];
+    __shared__ float sM[NW + 1][G], sL[NW + 1][G];
     __shared__ __align__(16) float sKn[D], sVn[D];
 
     /* ---- prologue: every input in flight at once ---- */
@@ -268,52 +268,47 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     q35_lds_barrier();
 
     /* ---- merge the waves (and the new token) ---- *
-     * wave 0, lane = 8 * head + source wave: the max and the weighted sum over
-     * the 8 lanes of a head on DPP, the new token folded in after. */
+     * wave w merges head w: every lane reads the 8 waves' (max, sum) of the
+     * head (broadcast LDS reads), forms the factors itself, and sums its 4
+     * dims of the 8 partial rows; lane 0 stores the head's (max, sum). */
     float *po = p.part_o + ((size_t)(g * p.n_chunks + c) * G) * D;
     float *pml = p.part_ml + ((size_t)(g * p.n_chunks + c) * G) * 2;
-    if (w == 0) {
-        const int hh = lane >> 3, s2 = lane & 7;
-        const float ms = sM[s2][hh], ls = sL[s2][hh];
-        float M = ms;
-        M = fmaxf(M, q35_dpp<0xB1>(M));
-        M = fmaxf(M, q35_dpp<0x4E>(M));
-        M = fmaxf(M, q35_dpp<0x141>(M));
-        const float mnew = last ? sM[NW][hh] : -INFINITY;
-        M = fmaxf(M, mnew);
-        const float f = (ms == -INFINITY) ? 0.0f : q35_exp(ms - M);
-        const float L = q35_sum8(ls * f);
-        sF[s2][hh] = f;
-        if (s2 == 0) {
-            const float fn = last ? q35_exp(mnew - M) : 0.0f;
-            sF[NW][hh] = fn;
-            pml[hh * 2] = M;
-            pml[hh * 2 + 1] = L + (last ? sL[NW][hh] * fn : 0.0f);
-        }
-    }
-    q35_lds_barrier();
     {
-        /* thread t: head t / 64, dims 4 (t % 64) .. +3 */
-        const int hh = t >> 6, d4 = 4 * lane;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int hh = w, d4 = 4 * lane;
+        float ms[NW];
+        const float mnew = last ? sM[NW][hh] : -INFINITY;
+        float M = mnew;
 #pragma unroll
         for (int s2 = 0; s2 < NW; s2++) {
+            ms[s2] = sM[s2][hh];
+            M = fmaxf(M, ms[s2]);
+        }
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < NW; s2++) {
+            const float f = (ms[s2] == -INFINITY) ? 0.0f : q35_exp(ms[s2] - M);
             const float4 v = *reinterpret_cast<const float4 *>(&sO[s2][hh * OS + d4]);
-            const float f = sF[s2][hh];
+            L = fmaf(sL[s2][hh], f, L);
             o.x = fmaf(v.x, f, o.x);
             o.y = fmaf(v.y, f, o.y);
             o.z = fmaf(v.z, f, o.z);
             o.w = fmaf(v.w, f, o.w);
         }
         if (last) {
+            const float f = q35_exp(mnew - M);
             const float4 v = *reinterpret_cast<const float4 *>(&sVn[d4]);
-            const float f = sF[NW][hh];
+            L = fmaf(sL[NW][hh], f, L);
             o.x = fmaf(v.x, f, o.x);
             o.y = fmaf(v.y, f, o.y);
             o.z = fmaf(v.z, f, o.z);
             o.w = fmaf(v.w, f, o.w);
         }
         *reinterpret_cast<float4 *>(po + hh * D + d4) = o;
+        if (lane == 0) {
+            pml[hh * 2] = M;
+            pml[hh * 2 + 1] = L;
+        }
     }
 }
 
