@@ -20,7 +20,11 @@
  * columns) inside the workgroup, so the layer is one launch with no
  * cross-workgroup handshake: splitting a head over workgroups would need an
  * agent-scope release / acquire per head, which costs more on this GPU than
- * the per-CU state traffic it spreads.
+ * the per-CU state traffic it spreads.  Inside the workgroup, each norm is
+ * one wave's sum: waves 0 / 1 / 2 convolve the head's q / k / v channels, two
+ * a lane (so the q and k norms need no cross-wave step), and wave 3 computes
+ * the gates and, at the end, the gated norm of all 128 outputs; the kernel
+ * has two barriers (conv results to the delta rule, outputs to the norm).
  *
  * Arithmetic: fp32 with FMA in the state update (the reference sums i in
  * ascending order without FMA; the difference is fp32 rounding).  The
@@ -45,36 +49,39 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     const int w = t >> 6, l = t & 63, half = l >> 5, r0 = 4 * (l & 31);
     float4 *sp = reinterpret_cast<float4 *>(p.state + ((size_t)h * VD + 8 * w) * KD) + l;
     float4 s[4];
-    /* conv inputs of this head's q (t<128), k (t<256), v (t<384) channels */
-    int ch = -1, kind = -1;
-    if (t < KD) {
-        ch = kh * KD + t;
-        kind = 0;
-    } else if (t < 2 * KD) {
-        ch = p.k_heads * KD + kh * KD + (t - KD);
-        kind = 1;
-    } else if (t < 2 * KD + VD) {
-        ch = 2 * p.k_heads * KD + h * VD + (t - 2 * KD);
-        kind = 2;
-    }
-    float xin[4] = {0.f, 0.f, 0.f, 0.f};
-    uint2 wv = make_uint2(0, 0);
-    if (ch >= 0) {
+    /* conv inputs: wave 0 the head's q channels, wave 1 its k channels,
+     * wave 2 its v channels, two adjacent channels a lane, so that each
+     * q / k norm is a sum over one wave */
+    const int kind = w < 3 ? w : -1;
+    int ch = 0;
+    if (kind == 0)
+        ch = kh * KD + 2 * l;
+    else if (kind == 1)
+        ch = p.k_heads * KD + kh * KD + 2 * l;
+    else if (kind == 2)
+        ch = 2 * p.k_heads * KD + h * VD + 2 * l;
+    float2 xin[4];
+    uint4 wv = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int k = 0; k < 4; k++) xin[k] = make_float2(0.f, 0.f);
+    if (kind >= 0) {
 #pragma unroll
         for (int k = 0; k < 3; k++)
-            if (tok - 3 + k >= 0) xin[k] = p.ring[(size_t)((tok - 3 + k) & 3) * rows + ch];
-        xin[3] = p.qkv[ch];
-        wv = *reinterpret_cast<const uint2 *>(p.conv_w + (size_t)ch * 4);
+            if (tok - 3 + k >= 0)
+                xin[k] = *reinterpret_cast<const float2 *>(p.ring + (size_t)((tok - 3 + k) & 3) * rows + ch);
+        xin[3] = *reinterpret_cast<const float2 *>(p.qkv + ch);
+        wv = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)ch * 4);
     }
-    float zv = 0.0f;
-    uint16_t nw = 0;
-    if (t < VD) {
-        zv = p.z[h * VD + t];
-        nw = p.norm_w[t];
+    /* the gated norm's inputs: wave 3 owns the head's 128 outputs, 2 a lane */
+    float2 zv = make_float2(0.f, 0.f);
+    uint32_t nw = 0;
+    if (w == 3) {
+        zv = *reinterpret_cast<const float2 *>(p.z + h * VD + 2 * l);
+        nw = *reinterpret_cast<const uint32_t *>(p.norm_w + 2 * l);
     }
     float ga = 0.f, gb = 0.f, gal = 0.f;
     uint16_t gdt = 0;
-    if (t == 2 * KD + VD) {
+    if (t == 3 * 64) {
         ga = p.a[h];
         gb = p.b[h];
         gal = p.A_log[h];
@@ -84,43 +91,44 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
 #pragma unroll
     for (int u = 0; u < 4; u++) s[u] = sp[64 * u];
     __shared__ float sq[KD], sk[KD], sv[VD], so[VD];
-    __shared__ double sred[4];
     __shared__ float sgate[2];
 
     /* ---- prologue: conv + SiLU, ring update, q/k norms, gates ---- */
-    float x = 0.0f;
-    if (ch >= 0) {
-        x = q35_conv_silu(xin, wv, tok);
+    if (kind >= 0) {
+        const float xa[4] = {xin[0].x, xin[1].x, xin[2].x, xin[3].x};
+        const float xb[4] = {xin[0].y, xin[1].y, xin[2].y, xin[3].y};
+        const float ya = q35_conv_silu(xa, make_uint2(wv.x, wv.y), tok);
+        const float yb = q35_conv_silu(xb, make_uint2(wv.z, wv.w), tok);
         /* ring slot token%4 takes the raw row; q/k channels are shared by
          * the two value heads of a key head, the even one writes them */
-        if (kind == 2 || (h & 1) == 0) p.ring[(size_t)(tok & 3) * rows + ch] = xin[3];
+        if (kind == 2 || (h & 1) == 0)
+            *reinterpret_cast<float2 *>(p.ring + (size_t)(tok & 3) * rows + ch) = xin[3];
+        float2 y = make_float2(ya, yb);
+        if (kind < 2) {
+#pragma clang fp contract(off)
+            double ss = (double)ya * ya + (double)yb * yb;
+            ss = q35_wave_sum(ss);
+            const float r = sqrtf((float)(ss / (double)KD) + 1e-6f);
+            if (kind == 0) {
+                y.x = ya / r * (1.0f / (float)KD);
+                y.y = yb / r * (1.0f / (float)KD);
+                *reinterpret_cast<float2 *>(&sq[2 * l]) = y;
+            } else {
+                y.x = ya / r * (1.0f / sqrtf((float)KD));
+                y.y = yb / r * (1.0f / sqrtf((float)KD));
+                *reinterpret_cast<float2 *>(&sk[2 * l]) = y;
+            }
+            if (p.qkv_post && (h & 1) == 0) *reinterpret_cast<float2 *>(p.qkv_post + ch) = y;
+        } else {
+            *reinterpret_cast<float2 *>(&sv[2 * l]) = y;
+            if (p.qkv_post) *reinterpret_cast<float2 *>(p.qkv_post + ch) = y;
+        }
     }
-    double ss = (kind == 0 || kind == 1) ? (double)x * x : 0.0;
-    ss = q35_wave_sum(ss);
-    if ((t & 63) == 0 && t < 2 * KD) sred[t >> 6] = ss;
-    if (t == 2 * KD + VD) {
+    if (t == 3 * 64) {
         float g, beta;
         q35_lin_gates(ga, gb, gal, gdt, &g, &beta);
         sgate[0] = expf(g);
         sgate[1] = beta;
-    }
-    q35_lds_barrier();
-    if (kind == 0 || kind == 1) {
-#pragma clang fp contract(off)
-        double tot = kind == 0 ? sred[0] + sred[1] : sred[2] + sred[3];
-        float r = sqrtf((float)(tot / (double)KD) + 1e-6f);
-        float y;
-        if (kind == 0) {
-            y = x / r * (1.0f / (float)KD);
-            sq[t] = y;
-        } else {
-            y = x / r * (1.0f / sqrtf((float)KD));
-            sk[t - KD] = y;
-        }
-        if (p.qkv_post && (h & 1) == 0) p.qkv_post[ch] = y;
-    } else if (kind == 2) {
-        sv[t - 2 * KD] = x;
-        if (p.qkv_post) p.qkv_post[ch] = x;
     }
     q35_lds_barrier();
 
@@ -164,18 +172,18 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     }
     q35_lds_barrier();
 
-    /* ---- RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749) ---- */
-    if (t < VD) {
-        double o2 = (double)so[t] * so[t];
-        o2 = q35_wave_sum(o2);
-        if ((t & 63) == 0) sred[t >> 6] = o2;
-    }
-    q35_lds_barrier();
-    if (t < VD) {
+    /* ---- RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749),
+     * wave 3, two outputs a lane ---- */
+    if (w == 3) {
 #pragma clang fp contract(off)
-        float r = sqrtf((float)((sred[0] + sred[1]) / (double)VD) + 1e-6f);
-        float sg = q35_sigmoid(zv);
-        p.out[h * VD + t] = so[t] / r * q35_bf2f(nw) * (zv * sg);
+        const float2 ov = *reinterpret_cast<const float2 *>(&so[2 * l]);
+        double o2 = (double)ov.x * ov.x + (double)ov.y * ov.y;
+        o2 = q35_wave_sum(o2);
+        const float r = sqrtf((float)(o2 / (double)VD) + 1e-6f);
+        float2 y;
+        y.x = ov.x / r * q35_bf2f((uint16_t)(nw & 0xffff)) * (zv.x * q35_sigmoid(zv.x));
+        y.y = ov.y / r * q35_bf2f((uint16_t)(nw >> 16)) * (zv.y * q35_sigmoid(zv.y));
+        *reinterpret_cast<float2 *>(p.out + h * VD + 2 * l) = y;
     }
 }
 
