@@ -63,6 +63,20 @@ __device__ __forceinline__ void load_v(VTile &vt, __amdgpu_buffer_rsrc_t rs, int
         vt.v[dt] = __builtin_bit_cast(s16x4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, off + dt * 512, 0, 2));
 }
 
+/* max of v over lanes l and l ^ 16 (l ^ 32): gfx950's row-swap moves.  With
+ * both operands v, permlane16_swap returns v's even rows in both rows of a
+ * row pair in one result and its odd rows in the other (permlane32_swap
+ * the same for the two halves), so the max of v and both results is the
+ * pair's max, with no LDS permute. */
+__device__ __forceinline__ float pair_max16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_max32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
+}
+
 /* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
  * into hi | lo columns, P*V on MFMA into acc. */
 __device__ __forceinline__ void attend_tile(const KTile &kt, VTile &vt, const bf16x8_t *sqb,
@@ -83,8 +97,8 @@ __device__ __forceinline__ void attend_tile(const KTile &kt, VTile &vt, const bf
         sv[i] = v;
         tmax = fmaxf(tmax, v);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = pair_max16(tmax);     /* max over lanes l, l ^ 16, l ^ 32, l ^ 48 */
+    tmax = pair_max32(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = q35_exp(m_run - m_new);   /* m_run = -inf -> 0 */
     const bool rescale = __any(m_new != m_run && m_run != -INFINITY);
