@@ -76,6 +76,16 @@ __device__ __forceinline__ float pair_max32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
 }
+/* the pair's sum: one result holds the lane's own value, the other its
+ * partner's */
+__device__ __forceinline__ float pair_sum16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_sum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 /* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
  * into hi | lo columns, P*V on MFMA into acc. */
@@ -248,8 +258,8 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     }
 
     /* ---- per-wave partial: l over the 4 lane groups; O hi + lo columns ---- */
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = pair_sum16(l_run);
+    l_run = pair_sum32(l_run);
     /* lane (n < 8, grp) holds dims 16dt + 4grp .. +3 of head n: one 16-byte
      * LDS store per dim block */
 #pragma unroll
@@ -389,7 +399,7 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
      * the 8-lane half, with i ^ 2, with i ^ 1) each flip one bit of i; a
      * lane keeps the half of its dims whose index bit matches its own and
      * adds the partner's copy of that half, so lane i ends with its row's
-     * total of dim i; the four rows are then summed across lanes */
+     * total of dim i; the four rows are then summed with two row swaps */
     const int li = lane & 15;
     float a8[8], a4[4], a2[2];
 #pragma unroll
@@ -408,8 +418,8 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
         a2[j] = (hi ? a4[j + 2] : a4[j]) + q35_dpp<0x4E>(hi ? a4[j] : a4[j + 2]);
     }
     float tot = ((li & 1) ? a2[1] : a2[0]) + q35_dpp<0xB1>((li & 1) ? a2[0] : a2[1]);
-    tot += __shfl_xor(tot, 16);
-    tot += __shfl_xor(tot, 32);
+    tot = pair_sum16(tot);
+    tot = pair_sum32(tot);
     if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = (tot / L) * q35_sigmoid(gate);
 }
 
