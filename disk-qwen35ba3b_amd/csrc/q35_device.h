@@ -100,6 +100,16 @@ __device__ __forceinline__ T q35_wave_sum(T v) {
     return (q35_readlane(v, 0) + q35_readlane(v, 16)) + (q35_readlane(v, 32) + q35_readlane(v, 48));
 }
 
+/* sum over each 32-lane half of a wave (fp32): the 16-lane row totals on
+ * DPP, then gfx950's permlane16 row swap, whose two results hold a lane's
+ * row total and the other row's of its half (all 64 lanes active) */
+__device__ __forceinline__ float q35_half_sum_rows(float v) {
+    v = q35_sum8(v);
+    v += q35_dpp<0x140>(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 /* sum over each 32-lane half of a wave, the half's total in each of its
  * lanes (all 64 lanes must be active) */
 template <typename T>
