@@ -76,17 +76,6 @@ __device__ __forceinline__ float pair_max32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
 }
-/* the pair's sum: one result holds the lane's own value, the other its
- * partner's */
-__device__ __forceinline__ float pair_sum16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float pair_sum32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 /* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
  * into hi | lo columns, P*V on MFMA into acc. */
 __device__ __forceinline__ void attend_tile(const KTile &kt, VTile &vt, const bf16x8_t *sqb,
@@ -258,8 +247,8 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
     }
 
     /* ---- per-wave partial: l over the 4 lane groups; O hi + lo columns ---- */
-    l_run = pair_sum16(l_run);
-    l_run = pair_sum32(l_run);
+    l_run = q35_psum16(l_run);
+    l_run = q35_psum32(l_run);
     /* lane (n < 8, grp) holds dims 16dt + 4grp .. +3 of head n: one 16-byte
      * LDS store per dim block */
 #pragma unroll
@@ -347,8 +336,7 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, q35_dpp<0x4E>(v));
     v = fmaxf(v, q35_dpp<0x141>(v));
     v = fmaxf(v, q35_dpp<0x140>(v));
-    return fmaxf(fmaxf(q35_readlane(v, 0), q35_readlane(v, 16)),
-                 fmaxf(q35_readlane(v, 32), q35_readlane(v, 48)));
+    return pair_max32(pair_max16(v));
 }
 __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
     const int h = blockIdx.x, g = h / G, hh = h % G, d0 = 16 * blockIdx.y;
@@ -418,8 +406,8 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
         a2[j] = (hi ? a4[j + 2] : a4[j]) + q35_dpp<0x4E>(hi ? a4[j] : a4[j + 2]);
     }
     float tot = ((li & 1) ? a2[1] : a2[0]) + q35_dpp<0xB1>((li & 1) ? a2[0] : a2[1]);
-    tot = pair_sum16(tot);
-    tot = pair_sum32(tot);
+    tot = q35_psum16(tot);
+    tot = q35_psum32(tot);
     if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = (tot / L) * q35_sigmoid(gate);
 }
 

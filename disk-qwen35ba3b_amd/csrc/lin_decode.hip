@@ -147,7 +147,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         mem[u] = m;
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) mem[u] = q35_half_sum_rows(mem[u]);   /* the column's 32 lanes */
+    for (int u = 0; u < 4; u++) mem[u] = q35_half_sum(mem[u]);   /* the column's 32 lanes */
     float o[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
 #pragma unroll
     for (int u = 0; u < 4; u++) sp[64 * u] = s[u];
 #pragma unroll
-    for (int u = 0; u < 4; u++) o[u] = q35_half_sum_rows(o[u]);
+    for (int u = 0; u < 4; u++) o[u] = q35_half_sum(o[u]);
     if ((l & 31) == 0) {
 #pragma unroll
         for (int u = 0; u < 4; u++) so[8 * w + 2 * u + half] = o[u];

@@ -91,34 +91,53 @@ __device__ __forceinline__ double q35_readlane(double v, int l) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
-/* sum over the 64 lanes of a wave, the total in every lane: 16-lane rows on
- * DPP, then the four row totals through readlane */
+/* Sums across 16-lane rows on gfx950's row swaps.  With both operands v,
+ * permlane16_swap returns, for each pair of rows (0, 1) and (2, 3), the
+ * even row's values in both rows of one result and the odd row's in both
+ * rows of the other (permlane32_swap: the lower and the upper half), so the
+ * sum of the two results is the pair's sum, in the same order in every lane
+ * of the pair.  No LDS permute and no scalar round trip. */
+__device__ __forceinline__ float q35_psum16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float q35_psum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ double q35_psum16(double v) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+    const auto rl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return __longlong_as_double((long long)(((uint64_t)rh[0] << 32) | rl[0])) +
+           __longlong_as_double((long long)(((uint64_t)rh[1] << 32) | rl[1]));
+}
+__device__ __forceinline__ double q35_psum32(double v) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+    const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return __longlong_as_double((long long)(((uint64_t)rh[0] << 32) | rl[0])) +
+           __longlong_as_double((long long)(((uint64_t)rh[1] << 32) | rl[1]));
+}
+
+/* sum over the 64 lanes of a wave, the total in every lane (all 64 lanes
+ * active): 16-lane row totals on DPP, then the two row swaps */
 template <typename T>
 __device__ __forceinline__ T q35_wave_sum(T v) {
     v = q35_sum8(v);
     v += q35_dpp<0x140>(v);
-    return (q35_readlane(v, 0) + q35_readlane(v, 16)) + (q35_readlane(v, 32) + q35_readlane(v, 48));
-}
-
-/* sum over each 32-lane half of a wave (fp32): the 16-lane row totals on
- * DPP, then gfx950's permlane16 row swap, whose two results hold a lane's
- * row total and the other row's of its half (all 64 lanes active) */
-__device__ __forceinline__ float q35_half_sum_rows(float v) {
-    v = q35_sum8(v);
-    v += q35_dpp<0x140>(v);
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    return q35_psum32(q35_psum16(v));
 }
 
 /* sum over each 32-lane half of a wave, the half's total in each of its
- * lanes (all 64 lanes must be active) */
+ * lanes (all 64 lanes active) */
 template <typename T>
 __device__ __forceinline__ T q35_half_sum(T v) {
     v = q35_sum8(v);
     v += q35_dpp<0x140>(v);
-    const T lo = q35_readlane(v, 0) + q35_readlane(v, 16);
-    const T hi = q35_readlane(v, 32) + q35_readlane(v, 48);
-    return (threadIdx.x & 32) ? hi : lo;
+    return q35_psum16(v);
 }
 
 /* The chunk GEMM's tiled X operand (written by its X prep and by the
