@@ -408,7 +408,7 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
     float tot = ((li & 1) ? a2[1] : a2[0]) + q35_dpp<0xB1>((li & 1) ? a2[0] : a2[1]);
     tot = q35_psum16(tot);
     tot = q35_psum32(tot);
-    if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = (tot / L) * q35_sigmoid(gate);
+    if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = tot * __builtin_amdgcn_rcpf(L) * q35_sigmoid_fast(gate);
 }
 
 }  // namespace

@@ -28,7 +28,12 @@
  *
  * Arithmetic: fp32 with FMA in the state update (the reference sums i in
  * ascending order without FMA; the difference is fp32 rounding).  The
- * conv, norms and gates keep the reference's operation order.
+ * gates keep the reference's operation order (their decay error would
+ * compound over the state's lifetime).  The SiLU and the output gate's
+ * sigmoid use the hardware exp / reciprocal, and the three RMS norms an
+ * fp32 square sum times the hardware reciprocal square root (about 1 ulp
+ * each against the reference's double sums and IEEE divisions): the gated
+ * norm is the kernel's tail and the conv the head of its dependent chain.
  */
 #include "q35_device.h"
 #include "q35_launch.h"
@@ -97,25 +102,22 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     if (kind >= 0) {
         const float xa[4] = {xin[0].x, xin[1].x, xin[2].x, xin[3].x};
         const float xb[4] = {xin[0].y, xin[1].y, xin[2].y, xin[3].y};
-        const float ya = q35_conv_silu(xa, make_uint2(wv.x, wv.y), tok);
-        const float yb = q35_conv_silu(xb, make_uint2(wv.z, wv.w), tok);
+        const float ya = q35_conv_silu_fast(xa, make_uint2(wv.x, wv.y), tok);
+        const float yb = q35_conv_silu_fast(xb, make_uint2(wv.z, wv.w), tok);
         /* ring slot token%4 takes the raw row; q/k channels are shared by
          * the two value heads of a key head, the even one writes them */
         if (kind == 2 || (h & 1) == 0)
             *reinterpret_cast<float2 *>(p.ring + (size_t)(tok & 3) * rows + ch) = xin[3];
         float2 y = make_float2(ya, yb);
         if (kind < 2) {
-#pragma clang fp contract(off)
-            double ss = (double)ya * ya + (double)yb * yb;
-            ss = q35_wave_sum(ss);
-            const float r = sqrtf((float)(ss / (double)KD) + 1e-6f);
+            const float ri = __builtin_amdgcn_rsqf(q35_wave_sum(ya * ya + yb * yb) * (1.0f / KD) + 1e-6f);
             if (kind == 0) {
-                y.x = ya / r * (1.0f / (float)KD);
-                y.y = yb / r * (1.0f / (float)KD);
+                y.x = ya * ri * (1.0f / (float)KD);
+                y.y = yb * ri * (1.0f / (float)KD);
                 *reinterpret_cast<float2 *>(&sq[2 * l]) = y;
             } else {
-                y.x = ya / r * (1.0f / sqrtf((float)KD));
-                y.y = yb / r * (1.0f / sqrtf((float)KD));
+                y.x = ya * ri * (1.0f / sqrtf((float)KD));
+                y.y = yb * ri * (1.0f / sqrtf((float)KD));
                 *reinterpret_cast<float2 *>(&sk[2 * l]) = y;
             }
             if (p.qkv_post && (h & 1) == 0) *reinterpret_cast<float2 *>(p.qkv_post + ch) = y;
@@ -175,14 +177,11 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     /* ---- RMSNormGated over the head's 128 outputs (src/attn_qwen.c:726-749),
      * wave 3, two outputs a lane ---- */
     if (w == 3) {
-#pragma clang fp contract(off)
         const float2 ov = *reinterpret_cast<const float2 *>(&so[2 * l]);
-        double o2 = (double)ov.x * ov.x + (double)ov.y * ov.y;
-        o2 = q35_wave_sum(o2);
-        const float r = sqrtf((float)(o2 / (double)VD) + 1e-6f);
+        const float ri = __builtin_amdgcn_rsqf(q35_wave_sum(ov.x * ov.x + ov.y * ov.y) * (1.0f / VD) + 1e-6f);
         float2 y;
-        y.x = ov.x / r * q35_bf2f((uint16_t)(nw & 0xffff)) * (zv.x * q35_sigmoid(zv.x));
-        y.y = ov.y / r * q35_bf2f((uint16_t)(nw >> 16)) * (zv.y * q35_sigmoid(zv.y));
+        y.x = ov.x * ri * (zv.x * q35_sigmoid_fast(zv.x) * q35_bf2f((uint16_t)(nw & 0xffff)));
+        y.y = ov.y * ri * (zv.y * q35_sigmoid_fast(zv.y) * q35_bf2f((uint16_t)(nw >> 16)));
         *reinterpret_cast<float2 *>(p.out + h * VD + 2 * l) = y;
     }
 }

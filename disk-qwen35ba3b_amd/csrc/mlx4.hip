@@ -113,7 +113,10 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
 
     /* the nibble words, scales and biases of RP rows; rows at and past R
      * (and dead lanes) point past the buffers and read zero, so every load
-     * is unconditional */
+     * is unconditional.  Nontemporal: a decode step reads each weight once,
+     * and streaming them through the cache would evict the delta-rule
+     * states and the cache rows the cores read next (40 whole layers at
+     * 32768 context: 1249 -> 1329 tokens/s) */
     struct Rows {
         u32x4_t w[RP][NCH];
         uint32_t sc[RP][NCH], bi[RP][NCH];
@@ -127,9 +130,9 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
                 const bool in = live[ch] && r0 + u < R;
                 const int kk = in ? (int)(k0 >> 3) : (int)(nel / 8);
                 const int gg = in ? (int)(k0 >> 6) : ng;
-                q.w[u][ch] = __builtin_amdgcn_raw_buffer_load_b128(vr, 4 * kk, 0, 0);
-                q.sc[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2 * gg, 0, 0);
-                q.bi[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(br, 2 * gg, 0, 0);
+                q.w[u][ch] = __builtin_amdgcn_raw_buffer_load_b128(vr, 4 * kk, 0, 2);
+                q.sc[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(sr, 2 * gg, 0, 2);
+                q.bi[u][ch] = __builtin_amdgcn_raw_buffer_load_b16(br, 2 * gg, 0, 2);
             }
     };
     /* x, and with x_norm its RMSNorm, once per workgroup: thread t holds
