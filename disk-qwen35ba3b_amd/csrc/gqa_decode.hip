@@ -37,7 +37,7 @@ constexpr int D = Q35_GQA_D, G = Q35_GQA_GROUP, RD = Q35_ROPE_DIMS;
 constexpr int NW = 8, NT = 64 * NW;   /* waves per workgroup, threads */
 constexpr int HPW = G / NW;           /* q heads normed per wave in the prologue */
 constexpr int MAX_CHUNKS = 256;
-constexpr int OS = D + 16;            /* sO head stride: head hq starts 16 hq banks on */
+constexpr int OS = D + 4;             /* sO head stride: the 8 heads' 16-byte stores of a dim block start 4 banks apart */
 static_assert(NW == G, "wave w merges q head w of the kv head");
 constexpr float SCALE = 0.0625f;      /* 1/sqrtf(256), src/attn_qwen.c:334 */
 struct KTile { bf16x8_t k[8]; };
@@ -75,6 +75,29 @@ __device__ __forceinline__ float pair_max16(float v) {
 __device__ __forceinline__ float pair_max32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(fmaxf(v, __uint_as_float(r[0])), __uint_as_float(r[1]));
+}
+/* q_norm + RoPE of one q head, as q35_norm_rope_head but with an fp32
+ * square sum and the hardware reciprocal square root (about 1 ulp against
+ * the double sum and IEEE division): q feeds the hi / lo bf16 split and
+ * the scores only, while the new k row, which the cache stores, keeps the
+ * reference's operation order. */
+__device__ __forceinline__ float4 norm_rope_fast(float4 x, uint2 w, float4 c, float4 s, int lane) {
+    const float ri = __builtin_amdgcn_rsqf(q35_wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w) * (1.0f / D) + 1e-6f);
+    float v[4] = {x.x, x.y, x.z, x.w};
+    const uint16_t wt[4] = {(uint16_t)(w.x & 0xffff), (uint16_t)(w.x >> 16),
+                            (uint16_t)(w.y & 0xffff), (uint16_t)(w.y >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = v[e] * ri * q35_bf2f(wt[e]);
+    const float cc[4] = {c.x, c.y, c.z, c.w}, sn[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float pr = q35_xor8(v[e]);
+        if (lane < RD / 8)
+            v[e] = v[e] * cc[e] - pr * sn[e];
+        else if (lane < RD / 4)
+            v[e] = pr * sn[e] + v[e] * cc[e];
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
 }
 /* One 16-position sub-tile: scores on MFMA, online-softmax update, P split
  * into hi | lo columns, P*V on MFMA into acc. */
@@ -192,7 +215,7 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
 #pragma unroll
     for (int hh = 0; hh < HPW; hh++) {
         const int qh = HPW * w + hh;
-        const float4 y = q35_norm_rope_head(xq[hh], wq, rc, rs, lane);
+        const float4 y = norm_rope_fast(xq[hh], wq, rc, rs, lane);
         *reinterpret_cast<float4 *>(&sQ[qh][d0]) = y;
         const float yy[4] = {y.x, y.y, y.z, y.w};
         s16x4_t hv, lv;
