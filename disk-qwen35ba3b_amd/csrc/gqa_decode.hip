@@ -340,10 +340,15 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
             o.z = fmaf(v.z, f, o.z);
             o.w = fmaf(v.w, f, o.w);
         }
-        *reinterpret_cast<float4 *>(po + hh * D + d4) = o;
+        const __amdgpu_buffer_rsrc_t ors =
+            __builtin_amdgcn_make_buffer_rsrc(q35_uniform_ptr(po), 0, G * D * 4, Q35_BUF_DW3);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, o), ors, (hh * D + d4) * 4, 0,
+                                               Q35_ST_SC1);
         if (lane == 0) {
-            pml[hh * 2] = M;
-            pml[hh * 2 + 1] = L;
+            const __amdgpu_buffer_rsrc_t mrs =
+                __builtin_amdgcn_make_buffer_rsrc(q35_uniform_ptr(pml), 0, G * 2 * 4, Q35_BUF_DW3);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), mrs, hh * 8, 0, Q35_ST_SC1);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(L), mrs, hh * 8 + 4, 0, Q35_ST_SC1);
         }
     }
 }
@@ -431,7 +436,11 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
     float tot = ((li & 1) ? a2[1] : a2[0]) + q35_dpp<0xB1>((li & 1) ? a2[0] : a2[1]);
     tot = q35_psum16(tot);
     tot = q35_psum32(tot);
-    if (lane < 16) p.attn_out[(size_t)h * D + d0 + lane] = tot * __builtin_amdgcn_rcpf(L) * q35_sigmoid_fast(gate);
+    if (lane < 16)
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __float_as_uint(tot * __builtin_amdgcn_rcpf(L) * q35_sigmoid_fast(gate)),
+            __builtin_amdgcn_make_buffer_rsrc(q35_uniform_ptr(p.attn_out), 0, p.heads * D * 4, Q35_BUF_DW3),
+            (h * D + d0 + lane) * 4, 0, Q35_ST_SC1);
 }
 
 }  // namespace

@@ -107,7 +107,9 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         /* ring slot token%4 takes the raw row; q/k channels are shared by
          * the two value heads of a key head, the even one writes them */
         if (kind == 2 || (h & 1) == 0)
-            *reinterpret_cast<float2 *>(p.ring + (size_t)(tok & 3) * rows + ch) = xin[3];
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, xin[3]),
+                __builtin_amdgcn_make_buffer_rsrc(q35_uniform_ptr(p.ring), 0, 4 * rows * 4, Q35_BUF_DW3),
+                ((tok & 3) * rows + ch) * 4, 0, Q35_ST_SC1);
         float2 y = make_float2(ya, yb);
         if (kind < 2) {
             const float ri = __builtin_amdgcn_rsqf(q35_wave_sum(ya * ya + yb * yb) * (1.0f / KD) + 1e-6f);
@@ -164,8 +166,14 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         a = fmaf(s[u].w, qq.w, a);
         o[u] = a;
     }
+    {
+        const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+            q35_uniform_ptr(p.state + (size_t)h * VD * KD), 0, VD * KD * 4, Q35_BUF_DW3);
 #pragma unroll
-    for (int u = 0; u < 4; u++) sp[64 * u] = s[u];
+        for (int u = 0; u < 4; u++)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, s[u]), srs,
+                                                   ((8 * w * KD) + 4 * (l + 64 * u)) * 4, 0, Q35_ST_SC1);
+    }
 #pragma unroll
     for (int u = 0; u < 4; u++) o[u] = q35_half_sum(o[u]);
     if ((l & 31) == 0) {
@@ -182,7 +190,9 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         float2 y;
         y.x = ov.x * ri * (zv.x * q35_sigmoid_fast(zv.x) * q35_bf2f((uint16_t)(nw & 0xffff)));
         y.y = ov.y * ri * (zv.y * q35_sigmoid_fast(zv.y) * q35_bf2f((uint16_t)(nw >> 16)));
-        *reinterpret_cast<float2 *>(p.out + h * VD + 2 * l) = y;
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, y),
+            __builtin_amdgcn_make_buffer_rsrc(q35_uniform_ptr(p.out), 0, p.v_heads * VD * 4, Q35_BUF_DW3),
+            (h * VD + 2 * l) * 4, 0, Q35_ST_SC1);
     }
 }
 
