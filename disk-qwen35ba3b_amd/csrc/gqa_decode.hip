@@ -354,11 +354,12 @@ __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
 }
 
 /* merge: one wave per (q head, 16 output dims), grid (heads, D/16).  Lane l
- * takes the chunks l, l + 64, ... (at most MAX_CHUNKS / 64 a lane) and loads
- * their (max, sum) and 16 output dims in one memory round trip; the maximum
- * and the weighted sum are wave reductions on DPP lanes and the 16 dim
- * totals one transposing reduction, with no LDS and no barrier. */
-constexpr int MCH = MAX_CHUNKS / 64;            /* chunks a lane, at most */
+ * takes the chunks l, l + 64, ... (at most MCH a lane: 2 for the split's
+ * usual P <= 128, whose instance carries no dead chunk slots, else
+ * MAX_CHUNKS / 64) and loads their (max, sum) and 16 output dims in one
+ * memory round trip; the maximum and the weighted sum are wave reductions
+ * on DPP lanes and the 16 dim totals one transposing reduction, with no LDS
+ * and no barrier. */
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, q35_dpp<0xB1>(v));
     v = fmaxf(v, q35_dpp<0x4E>(v));
@@ -366,6 +367,7 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, q35_dpp<0x140>(v));
     return pair_max32(pair_max16(v));
 }
+template <int MCH>
 __global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
     const int h = blockIdx.x, g = h / G, hh = h % G, d0 = 16 * blockIdx.y;
     const int lane = threadIdx.x;
@@ -467,6 +469,9 @@ extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) 
                        dim3(NT), 0, stream, *p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gqa_merge_kernel, dim3(p->heads, D / 16), dim3(64), 0, stream, *p);
+    if (p->n_chunks <= 128)
+        hipLaunchKernelGGL(gqa_merge_kernel<2>, dim3(p->heads, D / 16), dim3(64), 0, stream, *p);
+    else
+        hipLaunchKernelGGL(gqa_merge_kernel<MAX_CHUNKS / 64>, dim3(p->heads, D / 16), dim3(64), 0, stream, *p);
     return hipGetLastError();
 }
