@@ -141,10 +141,10 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
      * rsq(mean + 1e-6) times w (src/attn_qwen.c:142-157 computes the sum in
      * double and divides by the square root: about 1 ulp apart here, and
      * 40 whole layers at 32768 context 1370 -> 1422 tokens/s, the norm being
-     * on the projection launch's dependent path).  The result, scaled by the inverse fp8 nibble unit, goes
-     * to LDS laid out [chunk][q][lane] (float4 q of lane l's 32 columns), so
-     * each lane's reads below are conflict-free 16-byte rows.  Every slot is
-     * written, zeros past C. */
+     * on the projection launch's dependent path).  The result, scaled by the
+     * inverse fp8 nibble unit, goes to LDS laid out [chunk][q][lane] (float4 q
+     * of lane l's 32 columns), so each lane's reads below are conflict-free
+     * 16-byte rows.  Every slot is written, zeros past C. */
     constexpr int XQ = NCH * CHUNK / 4 / NT;
     __shared__ float4 sx[NCH * CHUNK / 4];
     __shared__ float sredf[NT / 64];
