@@ -78,30 +78,33 @@ __device__ __forceinline__ int wslot(int r, int h) { return h ^ (((r >> 2) ^ (r 
 
 /* x rows -> (optional RMSNorm) -> fp16 hi / lo in word order, tiled, and
  * the group sums of hi + lo.  One workgroup per token row (rows >= M: zeros);
- * thread t takes words t, t + 256, ... of the row. */
+ * thread t takes words t, t + 256, ... of the row.  The norm is an fp32
+ * square sum times the hardware rsq (about 1 ulp from the reference's double
+ * sum and division, src/attn_qwen.c:142-157, far below the hi / lo split's
+ * 22 bits). */
 __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const int nw = p.K / 8;
     const bool live = m < p.M;
     const float *x = p.x + (size_t)m * p.ldx;
-    __shared__ double sred[NT / 64];
+    __shared__ float sred[NT / 64];
 
-    float r = 1.0f;
+    float ri = 1.0f;
     if (p.norm_w) {
-        double ss = 0.0;
+        float ss = 0.0f;
         for (int v = t; v < nw; v += NT) {
             if (!live) break;
             const float4 a = *reinterpret_cast<const float4 *>(x + 8 * v);
             const float4 b = *reinterpret_cast<const float4 *>(x + 8 * v + 4);
             const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int j = 0; j < 8; j++) ss += (double)e[j] * e[j];
+            for (int j = 0; j < 8; j++) ss = fmaf(e[j], e[j], ss);
         }
         ss = q35_wave_sum(ss);
         if (lane == 0) sred[t >> 6] = ss;
         q35_lds_barrier();
         ss = (sred[0] + sred[1]) + (sred[2] + sred[3]);
-        r = sqrtf((float)(ss / (double)p.K) + 1e-6f);
+        ri = __builtin_amdgcn_rsqf(ss * (1.0f / (float)p.K) + 1e-6f);
     }
     for (int v = t; v < nw; v += NT) {
         float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
                 const uint32_t ww[4] = {wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
                 for (int j = 0; j < 8; j++)
-                    e[j] = e[j] / r * q35_bf2f((uint16_t)(ww[j >> 1] >> (16 * (j & 1))));
+                    e[j] = e[j] * ri * q35_bf2f((uint16_t)(ww[j >> 1] >> (16 * (j & 1))));
             }
         }
         bool over = false;
