@@ -137,14 +137,18 @@ int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate,
                               const uint16_t *qn_w, const uint16_t *kn_w,
                               float *attn_out, float *k_post, void *stream);
 /* Prefill of B tokens t0.. of a GQA layer (fp16 MFMA flash attention).
- * Allocates its workspace on first use or growth (not capturable then). */
+ * Allocates its workspace on first use or growth (not capturable then);
+ * growth frees the previous workspace, so a HIP graph captured before it
+ * must be captured again. */
 int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate,
                                const float *k, const float *v,
                                const uint16_t *qn_w, const uint16_t *kn_w,
                                float *attn_out, float *k_post, void *stream);
 /* Prefill of B tokens t0.. of a delta-rule layer (chunked form).  qkv_post
  * [B][conv_rows] receives the post-conv, normed values (may be NULL).
- * Allocates its workspace on first use or growth (not capturable then). */
+ * Allocates its workspace on first use or growth (not capturable then);
+ * growth frees the previous workspace, so a HIP graph captured before it
+ * must be captured again. */
 int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv,
                                const float *z, const float *a, const float *b,
                                const uint16_t *conv_w, const float *A_log,
