@@ -377,7 +377,7 @@ def run_gqa_prefill(args) -> int:
     roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
                 "traffic": load_traffic(f"gqa_prefill_t{T}"),
-                "kernel": "gqa prefill = prep_kernel + vprep_kernel + prefix_kernel + attn_kernel (fp16 MFMA)",
+                "kernel": "gqa prefill = prep_kernel (k rows, v blocks, prefix rows) + attn_kernel (fp16 MFMA)",
                 "launches": K, "us_per_launch": round(op_us, 2), "flops_per_launch": flops}
 
     cpu = None

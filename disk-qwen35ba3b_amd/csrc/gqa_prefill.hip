@@ -95,8 +95,10 @@ __device__ __forceinline__ size_t vw_index(int g, int kbt, int kb, int d, int sl
     return (((size_t)g * kbt + kb) * D + d) * 32 + (((slot >> 3) ^ ((d >> 2) & 3)) << 3) + (slot & 7);
 }
 
-__global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
-    const int b = 4 * blockIdx.x + (threadIdx.x >> 6), pos = p.t0 + b;
+/* k of the new tokens, one wave a token (4 a 256-thread block bx): q35's
+ * k norm and RoPE -> k_post, the fp16 key workspace and the bf16 cache */
+__device__ __forceinline__ void prep_rows(const Q35GqaPrefill &p, int bx) {
+    const int b = 4 * bx + (threadIdx.x >> 6), pos = p.t0 + b;
     const int lane = threadIdx.x & 63, d0 = lane * 4;
     if (b >= p.B) return;                   /* wave-uniform; no barrier follows */
     const float *rope = p.rope + (size_t)pos * RD;
@@ -136,8 +138,8 @@ __global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p) {
  * left alone: earlier positions belong to the cache, later ones are
  * workspace padding; a granule holding such keys (the block at t0 or at
  * t0 + B when those are not multiples of 32) is stored key by key. */
-__global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
-    const int kb = (p.t0 >> 5) + (int)blockIdx.x, g = blockIdx.y;
+__device__ __forceinline__ void vprep_block(const Q35GqaPrefill &p, int bx, int g) {
+    const int kb = (p.t0 >> 5) + bx;
     const int t = threadIdx.x;
     __shared__ float sv[32][D + 1];
     /* rows: key r of the block is position 32kb + r */
@@ -204,8 +206,8 @@ __global__ __launch_bounds__(256) void vprep_kernel(Q35GqaPrefill p) {
  * [0, t0) from the bf16 cache and padding positions [t0+B, 32*kbt) as
  * zeros.  Threads cover (kv head, row r of n_rows, dim); row r maps to
  * position r below t0, else to the padding. */
-__global__ void prefix_kernel(Q35GqaPrefill p, int n_rows) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void prefix_rows(const Q35GqaPrefill &p, int n_rows, int bx) {
+    const int64_t i = (int64_t)bx * 256 + threadIdx.x;
     if (i >= (int64_t)p.kv_heads * n_rows * D) return;
     const int g = (int)(i / ((int64_t)n_rows * D));
     const int r = (int)((i / D) % n_rows), d = (int)(i % D);
@@ -218,6 +220,22 @@ __global__ void prefix_kernel(Q35GqaPrefill p, int n_rows) {
     }
     p.kw[kw_index(g, p.kbt, pos, d)] = f16_bits(kf);
     p.vw[vw_index(g, p.kbt, pos >> 5, d, v_slot(pos & 31))] = f16_bits(vf);
+}
+
+/* the three set-up passes in one launch (they write disjoint workspace
+ * and cache elements; as three launches the two dispatch gaps and the
+ * smaller kernels' tails cost about as much as the work): blocks [0, nk)
+ * prep_rows, the next nvb * kv_heads blocks vprep_block, the rest
+ * prefix_rows.  Every branch is block-uniform, so vprep_block's barrier
+ * sees all of its block's threads. */
+__global__ __launch_bounds__(256) void prep_kernel(Q35GqaPrefill p, int nvb, int n_rows) {
+    const int nk = (p.B + 3) / 4, nv = nvb * p.kv_heads, bx = (int)blockIdx.x;
+    if (bx < nk)
+        prep_rows(p, bx);
+    else if (bx < nk + nv)
+        vprep_block(p, (bx - nk) % nvb, (bx - nk) / nvb);
+    else
+        prefix_rows(p, n_rows, bx - nk - nv);
 }
 
 /* LDS: per group, two stages of one 32-key block, each the K tile (16 KB,
@@ -710,23 +728,16 @@ extern "C" hipError_t q35_gqa_prefill(const Q35GqaPrefill *pin, hipStream_t stre
     if (p.heads != p.kv_heads * G || p.kv_heads != 2 || p.B < 1 || p.t0 < 0) return hipErrorInvalidValue;
     p.nqb = (p.B + 15) / 16;
     p.kbt = (p.t0 + p.B + 31) / 32;
-    hipLaunchKernelGGL(prep_kernel, dim3((p.B + 3) / 4), dim3(256), 0, stream, p);
+    /* value blocks of the new keys, and rows prep_rows / vprep_block leave:
+     * the prefix and the key padding */
+    const int nvb = ((p.t0 + p.B - 1) >> 5) - (p.t0 >> 5) + 1;
+    const int n_rows = p.t0 + (p.kbt * 32 - (p.t0 + p.B));
+    const int64_t nblk = (p.B + 3) / 4 + (int64_t)nvb * p.kv_heads +
+                         ((int64_t)p.kv_heads * n_rows * D + 255) / 256;
+    if (nblk > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prep_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, p, nvb, n_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    {
-        const int nvb = ((p.t0 + p.B - 1) >> 5) - (p.t0 >> 5) + 1;
-        hipLaunchKernelGGL(vprep_kernel, dim3(nvb, p.kv_heads), dim3(256), 0, stream, p);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
-    const int n_rows = p.t0 + (p.kbt * 32 - (p.t0 + p.B));    /* prefix + key padding */
-    if (n_rows > 0) {
-        const int64_t n = (int64_t)p.kv_heads * n_rows * D;
-        hipLaunchKernelGGL(prefix_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
-                           n_rows);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
     hipLaunchKernelGGL(attn_kernel, dim3((p.nqb + 1) / 2 * p.kv_heads), dim3(512), 0, stream, p);
     return hipGetLastError();
 }
