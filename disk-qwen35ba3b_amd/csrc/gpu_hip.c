@@ -62,7 +62,9 @@ static struct Plugin {
     float *h_states;           /* pinned staging of the host chunk entry */
     size_t h_states_cap;
     int scratch_rc;            /* q35_lin_scratch_init's result at init */
-    int *d_status, *h_status;  /* the prefill kernels' status word (Q35_STATUS_*) */
+    int *d_status, *h_status;  /* the prefill kernels' status words (Q35_STATUS_*): [0] the
+                                  device-pointer callers', [HOST_WORD] the host entries' */
+    int *d_status_cur;         /* the word the next prefill launch sets */
     float *d_backup;           /* a delta-rule layer's state and ring before a chunk */
 } P;
 
@@ -126,6 +128,7 @@ int ds4f_gpu_init(void) {
         set_err("status word allocation failed");
         return -1;
     }
+    P.d_status_cur = P.d_status;
     P.ok = 1;
     return 0;
 }
@@ -188,16 +191,19 @@ static int ensure_stage(size_t dbytes, size_t hbytes) {
     return 0;
 }
 
+/* the prefill workspace: grow-only, by at least half its size, so a
+ * sequence of growing requests reallocates a few times, not every call */
 static int ensure_ws(size_t bytes) {
     if (bytes <= P.ws_cap) return 0;
+    const size_t want = bytes > P.ws_cap + P.ws_cap / 2 ? bytes : P.ws_cap + P.ws_cap / 2;
     if (P.d_ws) {
         HIPCHK(hipStreamSynchronize(P.stream));
         hipFree(P.d_ws);
     }
     P.d_ws = NULL;
     P.ws_cap = 0;
-    HIPCHK(hipMalloc(&P.d_ws, bytes));
-    P.ws_cap = bytes;
+    HIPCHK(hipMalloc(&P.d_ws, want));
+    P.ws_cap = want;
     return 0;
 }
 
@@ -266,8 +272,14 @@ static int sync_layer(int L, int dir, int n_tokens) {
 }
 
 int ds4f_gpu_attn_sync(int L, int dir, int n_kv_tokens) {
-    if (!P.ok || !P.bound) return -1;
-    if (L >= P.g.n_layers) return -1;
+    if (!P.ok || !P.bound) {
+        set_err("plugin not bound");
+        return -1;
+    }
+    if (L >= P.g.n_layers) {
+        set_err("sync: layer %d outside [0, %d)", L, P.g.n_layers);
+        return -1;
+    }
     int lo = L < 0 ? 0 : L, hi = L < 0 ? P.g.n_layers : L + 1;
     for (int l = lo; l < hi; l++)
         if (sync_layer(l, dir, n_kv_tokens) != 0) return -1;
@@ -438,9 +450,14 @@ int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate, const 
     if (check_layer(L, DS4F_LAYER_GQA) != 0) return -1;
     if (t0 < 0 || B < 1 || t0 >= P.g.max_tokens) return 0;   /* src/attn_qwen.c:256 */
     if (B > P.g.max_tokens - t0) B = P.g.max_tokens - t0;
-    size_t kb, vb;
+    /* the first call reserves the fp16 K / V workspace of the whole cache
+     * (t0 + B = max_tokens), so the later chunks of a chunked prefill, whose
+     * workspace grows with t0 + B, neither reallocate nor invalidate a HIP
+     * graph captured after the first */
+    size_t kb, vb, kr, vr;
     q35_gqa_prefill_ws_bytes(t0, B, P.g.n_kv_heads, &kb, &vb);
-    if (ensure_ws(kb + vb) != 0) return -1;
+    q35_gqa_prefill_ws_bytes(0, P.g.max_tokens, P.g.n_kv_heads, &kr, &vr);
+    if (ensure_ws(kr + vr) != 0) return -1;
     Q35GqaPrefill p;
     memset(&p, 0, sizeof p);
     p.q_gate = q_gate;
@@ -460,7 +477,7 @@ int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate, const 
     p.t_tiles = P.t_tiles;
     p.heads = P.g.n_heads;
     p.kv_heads = P.g.n_kv_heads;
-    p.status = P.d_status;
+    p.status = P.d_status_cur;
     HIPCHK(q35_gqa_prefill(&p, pick(stream)));
     return 0;
 }
@@ -554,7 +571,7 @@ static int lin_prefill_launch(int L, int t0, int B, const float *qkv, const floa
     p.xw = xw;
     p.xsum = xsum;
     p.mpad = mpad;
-    p.status = P.d_status;
+    p.status = P.d_status_cur;
     HIPCHK(q35_lin_prefill(&p, pick(stream)));
     return 0;
 }
@@ -620,16 +637,36 @@ static int download(void *d_src, size_t bytes) {
     return 0;
 }
 
-/* the status word: cleared ahead of a host entry's launches, read after */
-static int status_clear(hipStream_t st) {
-    HIPCHK(hipMemsetAsync(P.d_status, 0, sizeof(int), st));
+/* The status words.  Word 0 is the device-pointer callers' (read and
+ * cleared by ds4f_hip_f16_status); the host entries switch the launches to
+ * their own word HOST_WORD for the duration of a call (host_status_begin
+ * clears it, host_status_end reads it and switches back), so a bit a
+ * device-pointer call left in word 0 is neither cleared nor reported by
+ * them. */
+enum { HOST_WORD = 16 };   /* 64 bytes past word 0 */
+static int status_clear(const int *word, hipStream_t st) {
+    HIPCHK(hipMemsetAsync((void *)word, 0, sizeof(int), st));
     return 0;
 }
-static int status_read(hipStream_t st, int *bits) {
-    HIPCHK(hipMemcpyAsync(P.h_status, P.d_status, sizeof(int), hipMemcpyDeviceToHost, st));
+static int status_read(const int *word, hipStream_t st, int *bits) {
+    HIPCHK(hipMemcpyAsync(P.h_status, word, sizeof(int), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
     *bits = *P.h_status;
     return 0;
+}
+static int host_status_begin(void) {
+    P.d_status_cur = P.d_status + HOST_WORD;
+    if (status_clear(P.d_status_cur, P.stream) != 0) {
+        P.d_status_cur = P.d_status;
+        return -1;
+    }
+    return 0;
+}
+/* reads the host word (when bits is not NULL) and switches back to word 0 */
+static int host_status_end(int *bits) {
+    int rc = bits ? status_read(P.d_status + HOST_WORD, P.stream, bits) : 0;
+    P.d_status_cur = P.d_status;
+    return rc;
 }
 
 int ds4f_hip_f16_status(void *stream, int clear) {
@@ -639,8 +676,9 @@ int ds4f_hip_f16_status(void *stream, int clear) {
     }
     hipStream_t st = pick(stream);
     int bits = 0;
-    if (status_read(st, &bits) != 0) return -1;
-    if (clear && bits && (status_clear(st) != 0 || hipStreamSynchronize(st) != hipSuccess)) return -1;
+    if (status_read(P.d_status, st, &bits) != 0) return -1;
+    if (clear && bits && (status_clear(P.d_status, st) != 0 || hipStreamSynchronize(st) != hipSuccess))
+        return -1;
     return bits;
 }
 
@@ -717,12 +755,14 @@ int ds4f_gpu_gqa_prefill(int L, int t0, int B, const float *q_gate, float *k, co
     if (upload(pc, 5, ob + kb, &dout) != 0) return fail_over(t0);
     float *d_attn = (float *)dout, *d_kpost = (float *)((char *)dout + ob);
     int bits = 0;
-    if (status_clear(P.stream) != 0 ||
-        ds4f_hip_gqa_prefill_async(L, t0, B, (const float *)dq, (const float *)dk,
+    if (host_status_begin() != 0) return fail_over(t0 + B);
+    if (ds4f_hip_gqa_prefill_async(L, t0, B, (const float *)dq, (const float *)dk,
                                    (const float *)dv, (const uint16_t *)dqn,
-                                   (const uint16_t *)dkn, d_attn, d_kpost, NULL) != 0 ||
-        status_read(P.stream, &bits) != 0)
+                                   (const uint16_t *)dkn, d_attn, d_kpost, NULL) != 0) {
+        host_status_end(NULL);
         return fail_over(t0 + B);
+    }
+    if (host_status_end(&bits) != 0) return fail_over(t0 + B);
     if (bits & Q35_STATUS_GQA_F16) {
         /* an operand beyond fp16 range: the tokens again on the decode
          * kernels (bf16 cache, fp32 q and weights), in order; the prefill
@@ -1002,6 +1042,7 @@ typedef struct LayerW {
     const uint16_t *qn, *kn, *conv_w, *dt_bias, *norm_w;
     const float *A_log;
     Q35Mlx4GemmJob gj[5];      /* the chunk GEMMs' projections, then the output (y set per call) */
+    int skip;                  /* incomplete in the trunk: every step and chunk is a silent skip */
 } LayerW;
 
 /* activations between the launches of one layer step, floats */
@@ -1043,6 +1084,39 @@ static void layers_free(void) {
     P.h_states_cap = 0;
     P.hidden = 0;
 }
+
+/* Layer L's trunk lacks a role that gqa_step / linear_step require
+ * (src/attn_qwen.c:96-97, :849-856, "incomplete graph: skip"): its weights
+ * are dropped and every step and chunk of it returns 0 with the state
+ * unchanged, as the reference's do.  Called by the trunk loader. */
+__attribute__((visibility("hidden"))) int ds4f_plugin_layer_skip(int L) {
+    if (!P.ok || P.disabled || !P.bound) {
+        set_err("plugin not bound or disabled");
+        return -1;
+    }
+    if (L < 0 || L >= P.g.n_layers) {
+        set_err("layer %d outside [0, %d)", L, P.g.n_layers);
+        return -1;
+    }
+    if (!P.lw) {
+        P.lw = (LayerW *)calloc((size_t)P.g.n_layers, sizeof(LayerW));
+        if (!P.lw) {
+            set_err("layer table allocation failed");
+            return -1;
+        }
+    }
+    LayerW *lw = &P.lw[L];
+    if (lw->d) {
+        HIPCHK(hipStreamSynchronize(P.stream));
+        hipFree(lw->d);
+    }
+    memset(lw, 0, sizeof *lw);
+    lw->skip = 1;
+    return 0;
+}
+
+/* a layer the trunk loader marked incomplete */
+static int layer_skipped(int L) { return P.lw && P.lw[L].skip; }
 
 static int mlx4_shape_ok(const Ds4fGpuMlx4W *m, int rows, int cols, const char *name) {
     if (!m->vals || !m->scales || m->rows != rows || m->cols != cols ||
@@ -1087,7 +1161,10 @@ int ds4f_gpu_attn_weights(int L, const Ds4fGpuLayerW *w) {
         set_err("plugin not bound or disabled");
         return -1;
     }
-    if (L < 0 || L >= P.g.n_layers || !w) return -1;
+    if (L < 0 || L >= P.g.n_layers || !w) {
+        set_err("layer weights: layer %d outside [0, %d) or no weights", L, P.g.n_layers);
+        return -1;
+    }
     const int kind = P.kind[L];
     if (kind != DS4F_LAYER_GQA && kind != DS4F_LAYER_LINEAR) {
         set_err("layer %d has no attention kind", L);
@@ -1236,9 +1313,12 @@ int ds4f_hip_attn_step_async(int L, int token, float *state, void *stream) {
         set_err("plugin not bound or disabled");
         return -1;
     }
-    if (L < 0 || L >= P.g.n_layers) return -1;
+    if (L < 0 || L >= P.g.n_layers) {
+        set_err("layer step: layer %d outside [0, %d)", L, P.g.n_layers);
+        return -1;
+    }
     const int kind = P.kind[L];
-    if (kind == DS4F_LAYER_NONE) return 0;                 /* src/attn_qwen.c:1264 */
+    if (kind == DS4F_LAYER_NONE || layer_skipped(L)) return 0;   /* src/attn_qwen.c:1264, :96-97, :849-856 */
     if (!P.lw || !P.lw[L].d) {
         set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
         return -1;
@@ -1277,8 +1357,12 @@ int ds4f_gpu_attn_step(int L, int token, float *state) {
         set_err("plugin not bound or disabled");
         return -1;
     }
-    if (L < 0 || L >= P.g.n_layers) return -1;
-    if (P.kind[L] == DS4F_LAYER_NONE || token < 0 || token >= P.g.max_tokens) return 0;
+    if (L < 0 || L >= P.g.n_layers) {
+        set_err("layer step: layer %d outside [0, %d)", L, P.g.n_layers);
+        return -1;
+    }
+    if (P.kind[L] == DS4F_LAYER_NONE || layer_skipped(L) || token < 0 || token >= P.g.max_tokens)
+        return 0;
     if (!P.lw || !P.lw[L].d) {
         set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
         return -1;
@@ -1357,14 +1441,18 @@ static int ensure_chunk(int B, ChunkWs *ws, int *mpad_out) {
     const int mpad = (B + mt - 1) / mt * mt;
     *mpad_out = mpad;
     if (mpad > P.chunk_cap) {
+        /* grow-only, by at least half, in whole token tiles */
+        int cap = P.chunk_cap + P.chunk_cap / 2;
+        cap = (cap + mt - 1) / mt * mt;
+        if (cap < mpad) cap = mpad;
         if (P.d_chunk) {
             HIPCHK(hipStreamSynchronize(P.stream));
             hipFree(P.d_chunk);
         }
         P.d_chunk = NULL;
         P.chunk_cap = 0;
-        HIPCHK(hipMalloc(&P.d_chunk, chunk_layout(mpad, NULL)));
-        P.chunk_cap = mpad;
+        HIPCHK(hipMalloc(&P.d_chunk, chunk_layout(cap, NULL)));
+        P.chunk_cap = cap;
     }
     chunk_layout(P.chunk_cap, ws);
     return 0;
@@ -1377,7 +1465,7 @@ static int chunk_gemm(const float *x, int ldx, const uint16_t *norm_w, int K, in
                       const Q35Mlx4GemmJob *jobs, int njobs, float *const *ys, const int *lds,
                       int accumulate, const ChunkWs *ws, hipStream_t st) {
     if (x) {
-        Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, mpad, K, ldx, P.d_status};
+        Q35Mlx4Xprep xp = {x, norm_w, ws->xw, ws->xsum, B, mpad, K, ldx, P.d_status_cur};
         HIPCHK(q35_mlx4_xprep(&xp, st));
     }
     Q35Mlx4Gemm g;
@@ -1403,9 +1491,12 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
         set_err("plugin not bound or disabled");
         return -1;
     }
-    if (L < 0 || L >= P.g.n_layers) return -1;
+    if (L < 0 || L >= P.g.n_layers) {
+        set_err("layer chunk: layer %d outside [0, %d)", L, P.g.n_layers);
+        return -1;
+    }
     const int kind = P.kind[L];
-    if (kind == DS4F_LAYER_NONE || B < 1) return 0;
+    if (kind == DS4F_LAYER_NONE || layer_skipped(L) || B < 1) return 0;
     if (!P.lw || !P.lw[L].d) {
         set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
         return -1;
@@ -1461,8 +1552,13 @@ int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {
         set_err("plugin not bound or disabled");
         return -1;
     }
-    if (L < 0 || L >= P.g.n_layers) return -1;
-    if (P.kind[L] == DS4F_LAYER_NONE || B < 1 || t0 < 0 || t0 >= P.g.max_tokens) return 0;
+    if (L < 0 || L >= P.g.n_layers) {
+        set_err("layer chunk: layer %d outside [0, %d)", L, P.g.n_layers);
+        return -1;
+    }
+    if (P.kind[L] == DS4F_LAYER_NONE || layer_skipped(L) || B < 1 || t0 < 0 ||
+        t0 >= P.g.max_tokens)
+        return 0;
     if (!P.lw || !P.lw[L].d) {
         set_err("layer %d has no weights on the device (ds4f_gpu_attn_weights)", L);
         return -1;
@@ -1497,9 +1593,13 @@ int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states) {
                  hipMemcpyAsync((char *)P.d_backup + sb, layer_conv(P.slot[L]), cb,
                                 hipMemcpyDeviceToDevice, P.stream) != hipSuccess)) ||
         hipMemcpyAsync(d_states, P.h_states, bytes, hipMemcpyHostToDevice, P.stream) != hipSuccess ||
-        status_clear(P.stream) != 0 || ds4f_hip_attn_chunk_async(L, t0, B, d_states, NULL) != 0 ||
-        status_read(P.stream, &bits) != 0)
+        host_status_begin() != 0)
         return fail_over(t0);
+    if (ds4f_hip_attn_chunk_async(L, t0, B, d_states, NULL) != 0) {
+        host_status_end(NULL);
+        return fail_over(t0);
+    }
+    if (host_status_end(&bits) != 0) return fail_over(t0);
     if (bits) {
         /* a GEMM or attention operand beyond fp16 range: the chunk again as
          * B layer steps on the decode kernels (fp32 activations, bf16 cache),

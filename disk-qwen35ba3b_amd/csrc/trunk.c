@@ -9,7 +9,9 @@
  * by name, 8-byte aligned).  The functions here take that list and payload
  * as they are and resolve the roles the attention steps read, by the same
  * name suffixes as the reference (first match wins, src/moe.c:425-490),
- * into a Ds4fGpuLayerW for ds4f_gpu_attn_weights.
+ * into a Ds4fGpuLayerW for ds4f_gpu_attn_weights.  A layer that lacks a
+ * role its step requires is skipped by every later step and chunk, as
+ * gqa_step / linear_step skip it (src/attn_qwen.c:96-97, :849-856).
  *
  * MLX 4-bit weights are U32 tensors of shape [rows, cols / 8]: the decoded
  * column count is dims[1] * 8 (src/attn_qwen.c:103-105), with BF16 scales
@@ -23,8 +25,9 @@
 /* the reference's dtype codes (src/moe.c:36-42) */
 enum { DT_F32 = 0, DT_BF16 = 4, DT_U32 = 5 };
 
-/* the plugin's error text (gpu_hip.c) */
+/* the plugin's error text and its incomplete-layer mark (gpu_hip.c) */
 void ds4f_plugin_set_err(const char *msg) __attribute__((visibility("hidden")));
+int ds4f_plugin_layer_skip(int L) __attribute__((visibility("hidden")));
 
 static int ends_with(const char *s, const char *suffix) {
     const size_t cap = sizeof(((Ds4fGpuTrunkTensor *)0)->name);
@@ -41,7 +44,7 @@ int ds4f_gpu_trunk_roles(const Ds4fGpuTrunkTensor *t, int n, Ds4fGpuTrunkRoles *
     int *all = (int *)r;
     for (size_t i = 0; i < sizeof *r / sizeof(int); i++) all[i] = -1;
     const RoleName names[] = {
-        {".input_layernorm.weight", &r->in_norm},
+        {".attn_norm.weight", &r->in_norm}, {".input_layernorm.weight", &r->in_norm},
         {".self_attn.q_proj.weight", &r->q[0]}, {".self_attn.q_proj.scales", &r->q[1]},
         {".self_attn.q_proj.biases", &r->q[2]},
         {".self_attn.k_proj.weight", &r->k[0]}, {".self_attn.k_proj.scales", &r->k[1]},
@@ -129,6 +132,13 @@ int ds4f_gpu_attn_weights_trunk(int L, const Ds4fGpuTrunkTensor *t, int n, const
     const int kind = ds4f_gpu_trunk_roles(t, n, &r);
     if (kind < 0 || !tr) return -1;
     if (kind == DS4F_LAYER_NONE) return 0;           /* no attention roles: nothing to upload */
+    /* the roles whose absence makes gqa_step / linear_step skip the layer
+     * (src/attn_qwen.c:96-97, :849-856: "incomplete graph: skip") */
+    const int complete = kind == DS4F_LAYER_GQA
+        ? r.q[0] >= 0 && r.k[0] >= 0 && r.v[0] >= 0 && r.o[0] >= 0 && r.q_norm >= 0 && r.k_norm >= 0
+        : r.qkv[0] >= 0 && r.z[0] >= 0 && r.a[0] >= 0 && r.b[0] >= 0 && r.conv >= 0 &&
+              r.out[0] >= 0 && r.norm >= 0 && r.A_log >= 0 && r.dt_bias >= 0;
+    if (!complete) return ds4f_plugin_layer_skip(L);
     Ds4fGpuLayerW w;
     memset(&w, 0, sizeof w);
     trunk_err[0] = 0;

@@ -137,16 +137,19 @@ int ds4f_hip_gqa_decode_async(int L, int token, const float *q_gate,
                               const uint16_t *qn_w, const uint16_t *kn_w,
                               float *attn_out, float *k_post, void *stream);
 /* Prefill of B tokens t0.. of a GQA layer (fp16 MFMA flash attention).
- * Allocates its workspace on first use or growth (not capturable then);
- * growth frees the previous workspace, so a HIP graph captured before it
- * must be captured again. */
+ * The first call allocates the fp16 K / V workspace for the whole cache
+ * (max_tokens positions: every later t0 + B fits) and is not capturable;
+ * later calls allocate nothing unless a delta-rule prefill has since grown
+ * the shared workspace, which frees the previous one, so a HIP graph
+ * captured before such growth must be captured again. */
 int ds4f_hip_gqa_prefill_async(int L, int t0, int B, const float *q_gate,
                                const float *k, const float *v,
                                const uint16_t *qn_w, const uint16_t *kn_w,
                                float *attn_out, float *k_post, void *stream);
 /* Prefill of B tokens t0.. of a delta-rule layer (chunked form).  qkv_post
  * [B][conv_rows] receives the post-conv, normed values (may be NULL).
- * Allocates its workspace on first use or growth (not capturable then);
+ * Allocates its workspace (sized by B) on first use or when B exceeds
+ * every earlier call's (not capturable then; growth is by at least half);
  * growth frees the previous workspace, so a HIP graph captured before it
  * must be captured again. */
 int ds4f_hip_lin_prefill_async(int L, int t0, int B, const float *qkv,
@@ -306,9 +309,17 @@ int ds4f_gpu_trunk_roles(const Ds4fGpuTrunkTensor *t, int n, Ds4fGpuTrunkRoles *
  * its payload tr (the layer's bytes of trunk.bin, as the engine streams
  * them, src/trunk.c).  MLX weights are U32 [rows, cols / 8] (decoded cols
  * dims[1] * 8, src/attn_qwen.c:103-105) with BF16 scales / biases; norms,
- * conv1d and dt_bias BF16; A_log F32.  A list with no attention roles
- * uploads nothing and returns 0; a missing role or a dtype other than
- * these returns -1 with the reason in ds4f_gpu_last_error. */
+ * conv1d and dt_bias BF16; A_log F32.  The input norm is the tensor named
+ * *.attn_norm.weight or *.input_layernorm.weight (src/moe.c:371-373).  A
+ * list with no attention roles uploads nothing and returns 0.  A list that
+ * lacks a role the layer's step requires (GQA: q/k/v/o_proj weights,
+ * q_norm, k_norm; linear: in_proj_qkv/z/a/b and out_proj weights, conv1d,
+ * norm, A_log, dt_bias) uploads nothing, returns 0 and marks the layer
+ * incomplete: every later ds4f_gpu_attn_step / _chunk of it (and their
+ * device-pointer forms) returns 0 with the states unchanged, as gqa_step
+ * and linear_step skip such a layer (src/attn_qwen.c:96-97, :849-856).  A
+ * dtype, rank or size other than these returns -1 with the reason in
+ * ds4f_gpu_last_error. */
 int ds4f_gpu_attn_weights_trunk(int L, const Ds4fGpuTrunkTensor *t, int n,
                                 const uint8_t *tr);
 
@@ -337,10 +348,14 @@ int ds4f_hip_attn_step_async(int L, int token, float *state, void *stream);
  * float32 summation order. */
 int ds4f_gpu_attn_chunk(int L, int t0, int B, float *const *states);
 /* The same with the states in device memory, [B][hidden] contiguous,
- * enqueued on `stream`.  Allocates its workspace on first use or growth
- * (not capturable then); growth frees the previous workspace, so a HIP
- * graph captured before it must be captured again -- a caller that
- * captures chunks runs its largest chunk once before capturing. */
+ * enqueued on `stream`.  Allocates its workspaces on first use or growth
+ * (not capturable then): the GEMM and delta-rule workspaces grow with B
+ * (by at least half), the GQA one is reserved for the whole cache on the
+ * first GQA chunk.  Growth frees the previous workspace, so a HIP graph
+ * captured before it must be captured again -- a caller that captures
+ * chunks first runs, outside the capture, one chunk of a GQA layer and
+ * one of a delta-rule layer at its largest B; no later chunk of at most
+ * that B (at any t0) allocates. */
 int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream);
 
 /* The prefill paths compute with fp16 operands (the GQA prefill's q, k, v
@@ -356,7 +371,15 @@ int ds4f_hip_attn_chunk_async(int L, int t0, int B, float *states, void *stream)
  * ds4f_hip_attn_chunk_async) read the word here: this synchronises
  * `stream` (NULL: the plugin's stream) and returns the bits set since the
  * last clear (0: every fp16 operand was in range; -1 on error); clear != 0
- * clears them.  Outputs of a flagged device-pointer call are not valid. */
+ * clears them.  The host entries keep bits that were already set when they
+ * start (they clear and report only their own), so a device-pointer
+ * caller's flag survives an intervening host-entry prefill.  A flagged
+ * device-pointer call's outputs are not valid, and neither is what it
+ * advanced in place: a GQA call's cache rows t0 .. t0+B-1, and a delta-rule
+ * call's recurrent state and conv ring, which it updated from the
+ * out-of-range operand.  A caller that wants to recompute such a call
+ * snapshots the layer's state (ds4f_gpu_attn_sync to the host, or its own
+ * device copy) before the call; the host entries do this themselves. */
 int ds4f_hip_f16_status(void *stream, int clear);
 
 /* Last error text of the plugin (static storage). */

@@ -408,7 +408,15 @@ def test_chunk_fp16_range_falls_back(kind):
     B ds4f_gpu_attn_step calls on a fresh binding of the same state, and
     matches the oracle's chunk to a relative RMS of 2e-3 (the activations
     reach about 1e5, so the bf16 cache rows' rounding is large in absolute
-    terms)."""
+    terms).  The host entry's flag stays in its own status word: the
+    device-pointer callers' word reads 0 after it; a device-pointer chunk
+    of the same planted layer sets bit 2 there, and a later host-entry
+    chunk neither clears nor adds to it."""
+    import torch
+
+    from ds4f_hip import lib as L
+    from ds4f_hip.attn import dptr
+
     t0, B = 5, 24
 
     def planted():
@@ -425,10 +433,20 @@ def test_chunk_fp16_range_falls_back(kind):
     try:
         assert ga.lib.ds4f_hip_f16_status(None, 1) >= 0
         got = ga.attn_chunk(0, t0, states)
-        bits = ga.lib.ds4f_hip_f16_status(None, 1)
+        assert ga.lib.ds4f_hip_f16_status(None, 0) == 0      # the host entry's word is its own
         if kind == 1:
             ga.sync(0, to_host=True)
             dev_S = ga.cache.lin[0].copy()
+        # a device-pointer chunk of the later tokens: flagged in word 0
+        d_states = torch.tensor(states[:8], device=torch.device("cuda:0"))
+        torch.cuda.synchronize()
+        L.check(ga.lib.ds4f_hip_attn_chunk_async(0, t0 + B, 8, dptr(d_states), None), "chunk async")
+        bits = ga.lib.ds4f_hip_f16_status(None, 0)
+        # a host-entry chunk after it keeps that bit (and adds nothing of its own)
+        ga.attn_chunk(0, t0 + B + 8, states[8:12])
+        bits_after = ga.lib.ds4f_hip_f16_status(None, 1)
+        assert ga.lib.ds4f_hip_f16_status(None, 0) == 0
+        del d_states
     finally:
         ga.close()
     ga2, _, _ = planted()
@@ -448,7 +466,7 @@ def test_chunk_fp16_range_falls_back(kind):
     mx, rr = _err(got, exp)
     _say(f"chunk kind {kind} with an fp16-range plant: status {bits}, |exp| max "
          f"{np.abs(exp).max():.3e}, against the oracle: max scaled err {mx:.3e} rel-rms {rr:.3e}")
-    assert bits & 2
+    assert bits & 2 and bits_after == bits
     assert np.array_equal(got, steps)
     assert rr <= ATOL
     if kind == 1:
@@ -465,8 +483,10 @@ def test_layer_steps_from_trunk(tmp_path):
     payloads, and uploaded with ds4f_gpu_attn_weights_trunk.  Three decode
     tokens through the four layers match the oracle's layer steps on the
     same weights, and bit for bit the same steps with the weights given to
-    ds4f_gpu_attn_weights directly.  A layer list missing a role is refused
-    with the role named."""
+    ds4f_gpu_attn_weights directly.  A layer list missing a role its step
+    requires marks the layer incomplete: its steps and chunks leave the
+    states unchanged, as gqa_step skips such a layer (src/attn_qwen.c:96-97);
+    a role of the wrong dtype is refused with the role named."""
     import ctypes
 
     from ds4f_hip import trunk as T
@@ -510,12 +530,28 @@ def test_layer_steps_from_trunk(tmp_path):
             _say(f"trunk-loaded stack token {n_past + s}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
             assert np.array_equal(got[s], direct[s])
-        # a layer without its k_norm: refused, the role named
+        # a layer without its k_norm: incomplete, so a silent skip (state
+        # unchanged, nothing of it on the device), as the reference's gqa_step
         tens, payload = tr[3]
         keep = [t for t in tens if not t.name.decode().endswith("k_norm.weight")]
         short = (T.TrunkTensor * len(keep))(*keep)
         assert ga_t.lib.ds4f_gpu_attn_weights_trunk(3, ctypes.cast(short, ctypes.c_void_p),
-                                                    len(keep), payload.ctypes.data) == -1
+                                                    len(keep), payload.ctypes.data) == 0
+        st = W.hidden_state(HID, 4, 500)
+        assert np.array_equal(ga_t.attn_step(3, n_past + 3, st), st)
+        sts = np.stack([W.hidden_state(HID, 4, 501 + i) for i in range(3)])
+        assert np.array_equal(ga_t.attn_chunk(3, n_past + 3, sts), sts)
+        # a role of the wrong dtype: refused, the role named
+        bad = (T.TrunkTensor * len(tens))(*tens)
+        for t in bad:
+            if t.name.decode().endswith("k_norm.weight"):
+                t.dtype = 0
+        assert ga_t.lib.ds4f_gpu_attn_weights_trunk(3, ctypes.cast(bad, ctypes.c_void_p),
+                                                    len(tens), payload.ctypes.data) == -1
         assert b"k_norm" in ga_t.lib.ds4f_gpu_last_error()
+        # the layer's full list again: the step runs as before
+        assert ga_t.lib.ds4f_gpu_attn_weights_trunk(3, ctypes.cast(tens, ctypes.c_void_p),
+                                                    len(tens), payload.ctypes.data) == 0
+        assert not np.array_equal(ga_t.attn_step(3, n_past + 3, st), st)
     finally:
         ga_t.close()

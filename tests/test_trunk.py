@@ -87,3 +87,28 @@ def test_roles_dispatch_and_first_match():
     assert lib.ds4f_gpu_trunk_roles(ctypes.cast(tens, ctypes.c_void_p), 1, ctypes.byref(roles)) == 0
     assert lib.ds4f_gpu_trunk_roles(ctypes.cast(tens, ctypes.c_void_p), 3, ctypes.byref(roles)) == 1
     assert roles.conv == 1
+
+
+def test_input_norm_names():
+    """The input norm is found under either name the reference maps to
+    attn_norm (src/moe.c:371-373), the first tensor in list order winning;
+    a linear layer's own norm (linear_attn.norm.weight) is not taken for it."""
+    lib = L.load()
+    for names, want in ((["model.layers.0.attn_norm.weight",
+                          "model.layers.0.linear_attn.conv1d.weight"], 0),
+                        (["model.layers.0.input_layernorm.weight",
+                          "model.layers.0.linear_attn.conv1d.weight"], 0),
+                        (["model.layers.0.linear_attn.norm.weight",
+                          "model.layers.0.attn_norm.weight",
+                          "model.layers.0.input_layernorm.weight",
+                          "model.layers.0.linear_attn.conv1d.weight"], 1),
+                        (["model.layers.0.linear_attn.norm.weight",
+                          "model.layers.0.post_attention_layernorm.weight",
+                          "model.layers.0.linear_attn.conv1d.weight"], -1)):
+        tens = (T.TrunkTensor * len(names))()
+        for i, n in enumerate(names):
+            tens[i].name = n.encode()
+        roles = T.TrunkRoles()
+        assert lib.ds4f_gpu_trunk_roles(ctypes.cast(tens, ctypes.c_void_p), len(names),
+                                        ctypes.byref(roles)) == 1
+        assert roles.in_norm == want, names
