@@ -113,7 +113,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="CPU-baseline sample budget (whole steps, at least one)")
+                    help="CPU-baseline sample budget (whole steps: at least 5 after a warm-up, "
+                         "more while within this budget)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="stack_decode", choices=["stack_decode", "gqa_prefill",
                                                                     "lin_prefill", "hbm_copy",
@@ -261,15 +262,18 @@ def run_stack_decode(args) -> int:
     cpu = None
     if want_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import numpy as np
         import oracle as O
         from ds4f_hip import workloads as W
         O.lib()
         wts = {}
         for Lr, kd in enumerate(kinds):
             wts[Lr] = W.gqa_weights(gq, seed, Lr) if kd == 2 else W.lin_weights(lg, seed, Lr)
-        done, spent = 0, 0.0
-        while done < 64 and (done == 0 or spent < args.cpu_seconds):
-            s, pos = done, N + done
+        def cpu_step(s):
+            """One decode step of the 40 layers on the oracle; returns the
+            seconds spent inside the oracle's bodies (activations drawn
+            outside the timed calls)."""
+            pos, spent = N + s, 0.0
             for Lr, kd in enumerate(kinds):
                 if kd == 2:
                     q, k, v = W.gqa_token(gq, seed, Lr, pos)
@@ -285,11 +289,20 @@ def run_stack_decode(args) -> int:
                                w.A_log, w.dt_bias, w.norm_w, lg.k_heads, lg.v_heads, lg.kd,
                                lg.vd)
                     spent += time.perf_counter() - c0
-            done += 1
-        cpu = {"value": round(done / spent, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"{done} decode steps of the same 40-layer stack at {N} context "
-                         f"(positions {N}..{N + done - 1}), C oracle gcc -O2, 1 thread, "
-                         f"{spent:.1f} s", "host": host_cpu()}
+            return spent
+
+        # one untimed warm-up step, then whole steps (at least 5, within the
+        # --cpu-seconds budget, at most 16): the median step time
+        cpu_step(0)
+        times = []
+        while len(times) < 16 and (len(times) < 5 or sum(times) < args.cpu_seconds):
+            times.append(cpu_step(len(times) + 1))
+        med = float(np.median(times))
+        cpu = {"value": round(1.0 / med, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"median of {len(times)} decode steps of the same 40-layer stack at {N} "
+                         f"context (positions {N + 1}..{N + len(times)}, after a warm-up step at "
+                         f"{N}), C oracle gcc -O2, 1 thread; step times {min(times):.2f}-"
+                         f"{max(times):.2f} s", "host": host_cpu()}
 
     sd.close()
     # the headline metric names the 32K context; another --ctx says its own
