@@ -232,9 +232,14 @@ def test_gqa_prefill_fp16_range_falls_back():
     bit for bit those of B ds4f_gpu_gqa_decode calls on a fresh binding, and
     match the oracle's serial body with bf16 cache rows (the decode path's
     row format) relative to their magnitude, which the planted value raises
-    to about 1e5.  Without the plant the status stays 0 and the fp16 path
-    matches the oracle as usual."""
-    from ds4f_hip.lib import load
+    to about 1e5.  Without the plant the fp16 path matches the oracle as
+    usual.  The host entry flags into a status word of its own, so the
+    device-pointer callers' word reads 0 after it either way; the
+    device-pointer prefill of the planted tokens sets bit 1 there."""
+    import torch
+
+    from ds4f_hip.attn import dptr
+    from ds4f_hip.lib import check, load
     lib = load()
     T = 40
     qn, kn = W.gqa_weights(GQ)
@@ -251,9 +256,22 @@ def test_gqa_prefill_fp16_range_falls_back():
                                 kn)
         bits = lib.ds4f_hip_f16_status(None, 1)
         ga.close()
+        assert bits == 0
         if plant:
             ga = GpuAttention([2], T + 16, KvCache(1, T + 16))
             dec = np.stack([ga.gqa_decode(0, b, q[b], k[b], vv[b], qn, kn)[0] for b in range(T)])
+            # the same tokens through the device-pointer prefill: flagged in word 0
+            dev = torch.device("cuda:0")
+            tq, tk, tv = (torch.tensor(np.ascontiguousarray(a.reshape(T, -1)), device=dev)
+                          for a in (q, k, vv))
+            tqn = torch.tensor(qn.view(np.int16), device=dev)
+            tkn = torch.tensor(kn.view(np.int16), device=dev)
+            tout = torch.empty((T, GQ.heads * GQ.head_dim), dtype=torch.float32, device=dev)
+            torch.cuda.synchronize()
+            check(lib.ds4f_hip_gqa_prefill_async(0, 0, T, dptr(tq), dptr(tk), dptr(tv), dptr(tqn),
+                                                 dptr(tkn), dptr(tout), None, None), "prefill async")
+            bits = lib.ds4f_hip_f16_status(None, 1)
+            del tq, tk, tv, tqn, tkn, tout
             ga.close()
             assert np.array_equal(out, dec)
             ref = np.empty_like(out)
