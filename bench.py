@@ -257,6 +257,16 @@ def run_stack_decode(args) -> int:
                 "kernel": "gqa decode = gqa_split_kernel + gqa_merge_kernel",
                 "launches": n_gqa_launch, "us_per_launch": round(gqa_us, 3),
                 "bytes_per_launch": int(gqa_bytes)}
+    # the committed kernel trace of this command (same launches, traced):
+    # the split and merge durations of the GQA graph's ops and the fraction
+    # they give; tracing lengthens each dispatch, so it sits below `frac`
+    traced = load_traced(f"gqa_decode_ctx{N}")
+    if traced:
+        roofline["rocprof_traced"] = {
+            "us_per_launch": traced["sum_of_means_us"],
+            "frac": round(gqa_bytes / (traced["sum_of_means_us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "traced_run_event_us_per_launch": traced.get("traced_run_event_us_per_launch"),
+            "source": f"profiles/gqa_decode_ctx{N}_rocprof.json"}
 
     # ---- CPU baseline: the oracle, one thread, same state and streams
     cpu = None
@@ -429,6 +439,16 @@ def run_gqa_prefill(args) -> int:
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
+
+
+def load_traced(name: str):
+    """The GQA graph's ops in the committed kernel trace of the stack
+    workload (profiles/<name>_rocprof.json, written from a rocprofv3 kernel
+    trace by ds4f_hip.trace; None when absent)."""
+    tpath = os.path.join(ROOT, "profiles", f"{name}_rocprof.json")
+    if os.path.exists(tpath):
+        return json.load(open(tpath))
+    return None
 
 
 def load_traffic(name: str):
