@@ -417,17 +417,17 @@ def run_gqa_prefill(args) -> int:
         kv = np.zeros((T, 2 * gq.kv_heads * gq.head_dim), np.float32)
         kv[:rows.shape[0]] = rows
         secs = []
-        for t in pos:
-            c0 = time.perf_counter()
-            O.gqa_body(kv, int(t), hq[t].reshape(-1), hk[t].reshape(-1), hv[t].reshape(-1), qn_h,
-                       kn_h, gq.heads, gq.kv_heads, gq.head_dim)
-            secs.append(time.perf_counter() - c0)
+        for t in pos:    # each position: the median of 5 calls after a warm-up call
+            secs.append(med_time(lambda: O.gqa_body(kv, int(t), hq[t].reshape(-1), hk[t].reshape(-1),
+                                                    hv[t].reshape(-1), qn_h, kn_h, gq.heads,
+                                                    gq.kv_heads, gq.head_dim))[0])
         a, b = np.polyfit(pos.astype(float), np.array(secs), 1)
         est = float(sum(a * t + b for t in range(T)))
         cpu = {"value": round(T / est, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"oracle gqa_body timed at {len(pos)} positions 0..{T - 1} of the same "
-                         f"prefill ({sum(secs):.1f} s), linear fit integrated over the "
-                         f"{T} serial calls the reference makes (est. {est:.1f} s)", "host": host_cpu()}
+               "sample": f"oracle gqa_body at {len(pos)} positions 0..{T - 1} of the same "
+                         f"prefill, each the median of 5 calls after a warm-up, linear fit "
+                         f"integrated over the {T} serial calls the reference makes "
+                         f"(est. {est:.1f} s)", "host": host_cpu()}
     ga.close()
     line = {"metric": f"GQA causal prefill tokens/s ({T} tokens, 16q/2kv d256, 1 layer)",
             "value": round(T / (op_us * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
@@ -439,6 +439,19 @@ def run_gqa_prefill(args) -> int:
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
+
+
+def med_time(fn, reps: int = 5, warm: int = 1):
+    """Median wall time (s) of `reps` calls of fn() after `warm` untimed
+    calls, and the list of times."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        c0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - c0)
+    return sorted(ts)[len(ts) // 2], ts
 
 
 def load_traced(name: str):
@@ -596,7 +609,7 @@ def run_layer_decode(args) -> int:
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O
-        reps_cpu, secs = 0, 0.0
+        times = []
         if gqa:
             kc, vc = W.gqa_cache(gq, N, seed, 0)
             half = gq.kv_heads * gq.head_dim
@@ -605,26 +618,30 @@ def run_layer_decode(args) -> int:
             kv[:N, half:] = vc.reshape(N, half)
             qn_h, kn_h = W.gqa_weights(gq, seed, 0)
             q, k, v = W.gqa_token(gq, seed, 0, N)
-            while reps_cpu == 0 or secs < min(args.cpu_seconds, 5.0):
+            O.gqa_body(kv, N, q.reshape(-1), k.reshape(-1).copy(), v.reshape(-1), qn_h, kn_h,
+                       gq.heads, gq.kv_heads, gq.head_dim)                 # warm-up
+            while len(times) < 5 or sum(times) < min(args.cpu_seconds, 5.0):
                 c0 = time.perf_counter()
                 O.gqa_body(kv, N, q.reshape(-1), k.reshape(-1).copy(), v.reshape(-1), qn_h, kn_h,
                            gq.heads, gq.kv_heads, gq.head_dim)
-                secs += time.perf_counter() - c0
-                reps_cpu += 1
+                times.append(time.perf_counter() - c0)
         else:
             wt = W.lin_weights(lg, seed, 0)
             S0 = W.lin_state(lg, seed, 0).astype(np.float32)
             ring = W.ring_from_history(lg, W.lin_conv_history(lg, seed, 0), pos)
             qkv, z, a, b = W.lin_token(lg, seed, 0, 0)
-            while reps_cpu == 0 or secs < min(args.cpu_seconds, 5.0):
+            O.lin_body(ring, S0, pos, qkv, z, a, b, wt.conv_w, wt.A_log, wt.dt_bias,
+                       wt.norm_w, lg.k_heads, lg.v_heads, lg.kd, lg.vd)         # warm-up
+            while len(times) < 5 or sum(times) < min(args.cpu_seconds, 5.0):
                 c0 = time.perf_counter()
                 O.lin_body(ring, S0, pos, qkv, z, a, b, wt.conv_w, wt.A_log, wt.dt_bias,
                            wt.norm_w, lg.k_heads, lg.v_heads, lg.kd, lg.vd)
-                secs += time.perf_counter() - c0
-                reps_cpu += 1
-        cpu = {"value": round(reps_cpu / secs, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"{reps_cpu} oracle {'gqa_body' if gqa else 'lin_body'} calls of the same "
-                         f"layer shape ({secs:.1f} s)", "host": host_cpu()}
+                times.append(time.perf_counter() - c0)
+        med = sorted(times)[len(times) // 2]
+        cpu = {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"median of {len(times)} oracle {'gqa_body' if gqa else 'lin_body'} calls "
+                         f"of the same layer shape after a warm-up call ({sum(times):.1f} s)",
+               "host": host_cpu()}
     ga.close()
     what = (f"GQA decode tokens/s (1 layer, 16q/2kv d256, n_past {N})" if gqa
             else "gated delta-rule decode tokens/s (1 layer, 32 heads 128x128)")
@@ -747,18 +764,20 @@ def run_lin_prefill(args) -> int:
         hq, hz, ha, hb = W.lin_tokens(lg, min(T, 4096), seed, 0)
         ring = np.zeros((4, lg.rows), np.float32)
         Sh = np.zeros((lg.v_heads, lg.kd, lg.vd), np.float32)
-        done, secs = 0, 0.0
-        while done < hq.shape[0] and (done == 0 or secs < args.cpu_seconds):
-            n = min(64, hq.shape[0] - done)
-            sl = slice(done, done + n)
+        done, times = 0, []
+        while done + 64 <= hq.shape[0] and (len(times) < 6 or sum(times) < args.cpu_seconds):
+            sl = slice(done, done + 64)
             c0 = time.perf_counter()
             O.lin_prefill(ring, Sh, done, hq[sl], hz[sl], ha[sl], hb[sl], wt.conv_w, wt.A_log,
                           wt.dt_bias, wt.norm_w, lg.k_heads, lg.v_heads, lg.kd, lg.vd)
-            secs += time.perf_counter() - c0
-            done += n
-        cpu = {"value": round(done / secs, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"oracle serial lin_body over the first {done} tokens of the same "
-                         f"prefill ({secs:.1f} s; per-token cost is position-independent)", "host": host_cpu()}
+            times.append(time.perf_counter() - c0)
+            done += 64
+        timed = times[1:]        # the first batch is the warm-up
+        med = sorted(timed)[len(timed) // 2]
+        cpu = {"value": round(64 / med, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"oracle serial lin_body over the first {done} tokens of the same prefill "
+                         f"in 64-token batches: the median of {len(timed)} batches after a warm-up "
+                         f"batch (per-token cost is position-independent)", "host": host_cpu()}
     ga.close()
     line = {"metric": f"gated delta-rule prefill tokens/s ({T} tokens, 32 heads 128x128, 1 layer)",
             "value": round(T / (op_us * 1e-6), 1), "unit": "tokens/s", "n_gpus": 1, "steps": K,
@@ -832,17 +851,12 @@ def run_mlx4_head(args) -> int:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O
         rows = 8192          # a row sample of the same weight; the cost is linear in rows
-        reps, secs = 0, 0.0
-        while reps == 0 or secs < min(args.cpu_seconds, 5.0):
-            c0 = time.perf_counter()
-            O.mlx4_matvec(vals[:rows * C // 8], scales[:rows * C // 64], biases[:rows * C // 64],
-                          rows, C, x)
-            secs += time.perf_counter() - c0
-            reps += 1
-        cpu = {"value": round(reps * rows / R / secs, 3), "unit": "matvecs/s", "cores": 1,
+        med, ts = med_time(lambda: O.mlx4_matvec(vals[:rows * C // 8], scales[:rows * C // 64],
+                                                 biases[:rows * C // 64], rows, C, x), reps=9)
+        cpu = {"value": round(rows / R / med, 3), "unit": "matvecs/s", "cores": 1,
                "kind": "port",
-               "sample": f"{reps} oracle matvecs of the first {rows} rows of the same weight "
-                         f"({secs:.1f} s), scaled to {R} rows", "host": host_cpu()}
+               "sample": f"oracle matvec of the first {rows} rows of the same weight, the median "
+                         f"of {len(ts)} calls after a warm-up, scaled to {R} rows", "host": host_cpu()}
     line = {"metric": "MLX 4-bit output-head matvec (248320 x 2048) matvecs/s", "value": round(1e6 / us, 1),
             "unit": "matvecs/s", "n_gpus": 1, "steps": K, "warmup": WU,
             "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
@@ -992,8 +1006,10 @@ def run_block_decode(args) -> int:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O
         O.lib()
-        done, spent = 0, 0.0
-        while done < 16 and (done == 0 or spent < args.cpu_seconds):
+        times = []
+        # step 0 is the warm-up; then at least 5 timed steps (more within the budget)
+        while len(times) < 16 and (len(times) < 6 or sum(times[1:]) < args.cpu_seconds):
+            done = len(times)
             st = states0[done].copy()
             c0 = time.perf_counter()
             for Lr, kd in enumerate(kinds):
@@ -1003,12 +1019,14 @@ def run_block_decode(args) -> int:
                 else:
                     st = O.lin_step(cache.conv[Lr], cache.lin[Lr], N + done, st, weights[Lr],
                                     lg.k_heads, lg.v_heads, lg.kd, lg.vd)
-            spent += time.perf_counter() - c0
-            done += 1
-        cpu = {"value": round(done / spent, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "sample": f"{done} decode steps of the same 40 whole layers at {N} context, C "
-                         f"oracle gcc -O2 (layer steps incl. the 4-bit projections), 1 thread, "
-                         f"{spent:.1f} s", "host": host_cpu()}
+            times.append(time.perf_counter() - c0)
+        timed = times[1:]
+        med = sorted(timed)[len(timed) // 2]
+        cpu = {"value": round(1.0 / med, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"median of {len(timed)} decode steps of the same 40 whole layers at {N} "
+                         f"context after a warm-up step, C oracle gcc -O2 (layer steps incl. the "
+                         f"4-bit projections), 1 thread; step times {min(timed):.2f}-{max(timed):.2f} s",
+               "host": host_cpu()}
 
     ga.close()
     line = {"metric": "attention-block decode tokens/s (40 layers, projections included), "
@@ -1119,10 +1137,8 @@ def run_block_prefill(args) -> int:
         ga.sync(-1, to_host=True, n_kv_tokens=T)
         st_host = states0.cpu().numpy()
         pos = np.linspace(0, T - 1, 6).astype(int)
-        secs = []
-        for t in pos:
+        def steps_at(t):
             st = st_host[t].copy()
-            c0 = time.perf_counter()
             for Lr, kd in enumerate(kinds):
                 if kd == 2:
                     st = O.gqa_step(cache.kv[Lr], int(t), st, weights[Lr], gq.heads, gq.kv_heads,
@@ -1130,13 +1146,18 @@ def run_block_prefill(args) -> int:
                 else:
                     st = O.lin_step(cache.conv[Lr], cache.lin[Lr], int(t), st, weights[Lr],
                                     lg.k_heads, lg.v_heads, lg.kd, lg.vd)
-            secs.append(time.perf_counter() - c0)
+
+        # each position: the median of 5 passes over the 40 layers after a
+        # warm-up pass (a pass at t rewrites position t's rows and advances
+        # the delta-rule states: the cost, not the values, is what is timed)
+        secs = [med_time(lambda: steps_at(int(t)))[0] for t in pos]
         a, b = np.polyfit(pos.astype(float), np.array(secs), 1)
         est = float(sum(a * t + b for t in range(T)))
         cpu = {"value": round(T / est, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"C oracle (gcc -O2, 1 thread) 40 whole layer steps at {len(pos)} "
-                         f"positions 0..{T - 1} ({sum(secs):.1f} s), linear fit integrated "
-                         f"over the {T} serial steps of the reference's chunk (est. {est:.0f} s)", "host": host_cpu()}
+                         f"positions 0..{T - 1}, each the median of 5 passes after a warm-up, "
+                         f"linear fit integrated over the {T} serial steps of the reference's "
+                         f"chunk (est. {est:.0f} s)", "host": host_cpu()}
 
     ga.close()
     line = {"metric": f"attention-block prefill tokens/s ({T} tokens, 40 layers, projections "
