@@ -84,14 +84,16 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         zv = *reinterpret_cast<const float2 *>(p.z + h * VD + 2 * l);
         nw = *reinterpret_cast<const uint32_t *>(p.norm_w + 2 * l);
     }
-    float ga = 0.f, gb = 0.f, gal = 0.f;
-    uint16_t gdt = 0;
-    if (t == 3 * 64) {
-        ga = p.a[h];
-        gb = p.b[h];
-        gal = p.A_log[h];
-        gdt = p.dt_bias[h];
-    }
+    /* the head's gate inputs, at addresses uniform over the workgroup: read
+     * by every thread as scalar loads, which the vector-load waits do not
+     * cover (dt_bias as the 4-byte-aligned word that holds it: the scalar
+     * unit reads whole dwords).  Loaded in the gate lane's branch, dt_bias
+     * was a vector load whose bf16 conversion the compiler placed in the
+     * branch, so wave 3 waited for all of its loads before requesting its
+     * state, one memory round trip late. */
+    const float ga = p.a[h], gb = p.b[h], gal = p.A_log[h];
+    const int dt_hi = (int)((reinterpret_cast<uintptr_t>(p.dt_bias + h) >> 1) & 1);
+    const uint16_t gdt = (uint16_t)(*reinterpret_cast<const uint32_t *>(p.dt_bias + h - dt_hi) >> (16 * dt_hi));
 
 #pragma unroll
     for (int u = 0; u < 4; u++) s[u] = sp[64 * u];
