@@ -208,8 +208,6 @@ def run_stack_decode(args) -> int:
     sd = StackDecode(N, T, seed, host_cache=want_cpu)
     lib, ga, cache, layers, kinds = sd.lib, sd.ga, sd.cache, sd.layers, sd.kinds
     gq, lg = sd.gq, sd.lg
-    if want_cpu:
-        ga.sync(-1, to_host=True, n_kv_tokens=N)       # initial state for the CPU sample
 
     graphs = sd.capture(range(T))
     torch.cuda.synchronize()
@@ -268,9 +266,15 @@ def run_stack_decode(args) -> int:
             "traced_run_event_us_per_launch": traced.get("traced_run_event_us_per_launch"),
             "source": f"profiles/gqa_decode_ctx{N}_rocprof.json"}
 
-    # ---- CPU baseline: the oracle, one thread, same state and streams
+    # ---- CPU baseline: the oracle, one thread, same state and streams.  The
+    # starting state goes to the host only now, regenerated in place on the
+    # device: a device -> host sync of the caches before the timed steps left
+    # them about 3 % slower (20-step runs, with or without 200 ms of other GPU
+    # work or 50 warm-up steps in between)
     cpu = None
     if want_cpu:
+        sd.synth_state()
+        ga.sync(-1, to_host=True, n_kv_tokens=N)
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import numpy as np
         import oracle as O
@@ -941,25 +945,27 @@ def run_block_decode(args) -> int:
 
     cache = KvCache(40, max_tokens) if want_cpu else None
     ga = GpuAttention(kinds, max_tokens, cache)
-    for Lr, kd in enumerate(kinds):
-        if kd == 2:
-            L.check(lib.ds4f_hip_synth_gqa_cache(Lr, N, seed, S.tid(S.GQA_KCACHE, Lr),
-                                                 S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
-        else:
-            L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr), None),
-                    "synth state")
-            L.check(lib.ds4f_hip_synth_conv_history(Lr, N, seed, S.tid(S.LIN_CONVSTATE, Lr),
-                                                    None), "synth conv")
+
+    def synth_start():
+        """The layers' caches and states and the per-step hidden states,
+        generated in place from the seed (the same values every call)"""
+        for Lr, kd in enumerate(kinds):
+            if kd == 2:
+                L.check(lib.ds4f_hip_synth_gqa_cache(Lr, N, seed, S.tid(S.GQA_KCACHE, Lr),
+                                                     S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
+            else:
+                L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr),
+                                                     None), "synth state")
+                L.check(lib.ds4f_hip_synth_conv_history(Lr, N, seed, S.tid(S.LIN_CONVSTATE, Lr),
+                                                        None), "synth conv")
+        for s in range(T):
+            L.check(lib.ds4f_hip_synth(dptr(states[s]), H, 0, 0, 0.0, 1.0, seed,
+                                       S.tid(S.BLK_STATE, 0, s), None), "synth state")
 
     weights, weight_bytes, _ = register_block_weights(ga, kinds, H, seed, dev, want_cpu)
     states = torch.empty((T, H), dtype=torch.float32, device=dev)
-    for s in range(T):
-        L.check(lib.ds4f_hip_synth(dptr(states[s]), H, 0, 0, 0.0, 1.0, seed,
-                                   S.tid(S.BLK_STATE, 0, s), None), "synth state")
+    synth_start()
     torch.cuda.synchronize()
-    if want_cpu:
-        ga.sync(-1, to_host=True, n_kv_tokens=N)
-        states0 = states.cpu().numpy()
 
     def launch_step(s, stream):
         for Lr in range(40):
@@ -1003,6 +1009,12 @@ def run_block_decode(args) -> int:
 
     cpu = None
     if want_cpu:
+        # the starting caches, states and hidden rows go to the host only
+        # now, regenerated in place (a device -> host sync before the timed
+        # steps leaves them slower, as in the stack workload)
+        synth_start()
+        ga.sync(-1, to_host=True, n_kv_tokens=N)
+        states0 = states.cpu().numpy()
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O
         O.lib()

@@ -47,17 +47,7 @@ class StackDecode:
         self.cache = KvCache(n_layers, self.max_tokens) if host_cache else None
         self.ga = GpuAttention(self.kinds, self.max_tokens, self.cache)
         lib, gq, lg = self.lib, self.gq, self.lg
-
-        for Lr, kd in enumerate(self.kinds):
-            if kd == _L.LAYER_GQA:
-                _L.check(lib.ds4f_hip_synth_gqa_cache(Lr, ctx, seed, S.tid(S.GQA_KCACHE, Lr),
-                                                      S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
-            else:
-                _L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr),
-                                                      None), "synth state")
-                _L.check(lib.ds4f_hip_synth_conv_history(Lr, ctx, seed,
-                                                         S.tid(S.LIN_CONVSTATE, Lr), None),
-                         "synth conv")
+        self.synth_state()
 
         def synth(n, dtype, dist, p0, p1, tid, t=None):
             if t is None:
@@ -102,6 +92,22 @@ class StackDecode:
                 d["out"] = torch.empty((T, nz), dtype=torch.float32, device=dev)
             self.layers.append(d)
         torch.cuda.synchronize()
+
+    def synth_state(self) -> None:
+        """The layers' starting state on the device, generated in place from
+        the seed: the GQA caches' ctx rows, the delta-rule states and conv
+        rings (the same values every call, so a run can put it back)."""
+        lib, ctx, seed = self.lib, self.ctx, self.seed
+        for Lr, kd in enumerate(self.kinds):
+            if kd == _L.LAYER_GQA:
+                _L.check(lib.ds4f_hip_synth_gqa_cache(Lr, ctx, seed, S.tid(S.GQA_KCACHE, Lr),
+                                                      S.tid(S.GQA_VCACHE, Lr), None), "synth kv")
+            else:
+                _L.check(lib.ds4f_hip_synth_lin_state(Lr, 0.05, seed, S.tid(S.LIN_STATE, Lr),
+                                                      None), "synth state")
+                _L.check(lib.ds4f_hip_synth_conv_history(Lr, ctx, seed,
+                                                         S.tid(S.LIN_CONVSTATE, Lr), None),
+                         "synth conv")
 
     def launch_layer(self, Lr: int, s: int, stream) -> None:
         """Enqueue layer Lr of step s on `stream` (a ctypes void pointer)."""
