@@ -46,8 +46,6 @@
 namespace {
 
 constexpr int KD = 128, VD = 128, C = 64;
-constexpr int XS = KD + 4;     /* LDS row stride (floats) of K / Q tiles: conflict-free b128 */
-constexpr int AS = C + 4;      /* LDS row stride of A and of the Delta tile */
 
 __device__ __forceinline__ f32x4_t mfma4(float a, float b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -130,6 +128,11 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
     }
 }
 
+/* float offset of (row r, column k) in a [rows][128] / [rows][64] tile
+ * stored with granule swizzle g ^ (r % 16) */
+__device__ __forceinline__ int sw128(int r, int k) { return r * KD + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
+__device__ __forceinline__ int sw64(int r, int k) { return r * C + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
+
 /* 16x16 blocks of a 64x64 triangle: index of block (a, c), a <= c, among the
  * 10 blocks on and above the diagonal */
 __device__ __forceinline__ int blk_q(int a, int c) { return a * (9 - a) / 2 + (c - a); }
@@ -161,8 +164,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     }
 
     /* K and Q rows, later A^T of both value heads, later T of both */
-    __shared__ __align__(16) float sbuf[2 * C * XS];
-    float *sK = sbuf, *sQ = sbuf + C * XS;
+    __shared__ __align__(16) float sbuf[2 * C * KD];
+    float *sK = sbuf, *sQ = sbuf + C * KD;
     __shared__ double sG[2][C];
     __shared__ float sBeta[2][C];
 
@@ -201,8 +204,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
             kv = *reinterpret_cast<const float4 *>(row + KH * KD + kh * KD + c4);
             qv = *reinterpret_cast<const float4 *>(row + kh * KD + c4);
         }
-        *reinterpret_cast<float4 *>(&sK[r * XS + c4]) = kv;
-        *reinterpret_cast<float4 *>(&sQ[r * XS + c4]) = qv;
+        *reinterpret_cast<float4 *>(&sK[sw128(r, c4)]) = kv;
+        *reinterpret_cast<float4 *>(&sQ[sw128(r, c4)]) = qv;
     }
     q35_lds_barrier();
 
@@ -218,8 +221,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int blk = 0; blk < KD / 16; blk++) {
-            const float4 xa = *reinterpret_cast<const float4 *>(&X[(16 * tr + l16) * XS + 16 * blk + 4 * lq]);
-            const float4 yb = *reinterpret_cast<const float4 *>(&sK[(16 * tc + l16) * XS + 16 * blk + 4 * lq]);
+            const float4 xa = *reinterpret_cast<const float4 *>(&X[sw128(16 * tr + l16, 16 * blk + 4 * lq)]);
+            const float4 yb = *reinterpret_cast<const float4 *>(&sK[sw128(16 * tc + l16, 16 * blk + 4 * lq)]);
 #pragma unroll
             for (int e = 0; e < 4; e++) acc = mfma4(el(xa, e), el(yb, e), acc);
         }
@@ -374,16 +377,16 @@ struct ScanLds {
     float P[C * C];                    /* Pm [t][s] (sw64); tiles above the diagonal unread */
     float G1[Q35_LIN_GVEC];            /* the chunk's gate vector, for exp(G) and beta (phase 1) */
     float G2[Q35_LIN_GVEC];            /* the same, for exp(G_C - G) and exp(G_C) (phase 2) */
-    float S[16 * XS];                  /* state block [j][i] */
-    float X[16 * AS];                  /* X [j][t] */
-    float D[16 * AS];                  /* Delta [j][t] */
+    float S[16 * KD];                  /* state block [j][i] (sw128) */
+    float X[16 * C];                   /* X [j][t] (sw64) */
+    float D[16 * C];                   /* Delta [j][t] (sw64) */
 };
 static_assert(Q35_LIN_GVEC == 256, "a gate vector is four 64-float quarters, one per copy wave");
 
-/* float offset of (row r, column k) in a [rows][128] / [rows][64] tile
- * stored with granule swizzle g ^ (r % 16) */
-__device__ __forceinline__ int sw128(int r, int k) { return r * KD + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
-__device__ __forceinline__ int sw64(int r, int k) { return r * C + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
+/* LDS row of V slice row t: rows t and t ^ 1 swap where bit 2 of t is set,
+ * so the X update's reads of rows r and r + 4 (one 32-lane half of a wave)
+ * fall in the two different 16-bank halves (the map is its own inverse) */
+__device__ __forceinline__ int v_row(int t) { return t ^ ((t >> 2) & 1); }
 
 struct ScanGeo {
     int h, jb, kh, VH, KH, rows;
@@ -424,7 +427,7 @@ struct ScanCopy {
     /* one copy of the V slice (16 rows of 16 floats) */
     __device__ __forceinline__ void v(int c) const {
         const __amdgpu_buffer_rsrc_t rs = rows(c);
-        const int r = 16 * dw + (lane >> 2);
+        const int r = v_row(16 * dw + (lane >> 2));      /* the row this lane's LDS slot holds */
         q35_dma16(rs, __builtin_amdgcn_readfirstlane(lV + 1024 * dw),
                   (uint32_t)((r * g.rows + 2 * g.KH * KD + g.h * VD + 16 * g.jb + 4 * (lane & 3)) * 4), 0);
     }
@@ -525,7 +528,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int idx = u * 256 + t, jj = idx >> 5, i4 = (idx & 31) * 4;
-        *reinterpret_cast<float4 *>(&L.S[jj * XS + i4]) =
+        *reinterpret_cast<float4 *>(&L.S[sw128(jj, i4)]) =
             *reinterpret_cast<const float4 *>(state + (size_t)jj * KD + i4);
     }
     q35_lds_barrier();                                       /* B0 */
@@ -538,7 +541,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
         for (int blk = 0; blk < 8; blk++) {
             const int k = 16 * blk + 4 * lq;
-            const float4 sb = *reinterpret_cast<const float4 *>(&L.S[l16 * XS + k]);
+            const float4 sb = *reinterpret_cast<const float4 *>(&L.S[sw128(l16, k)]);
             const float4 ka = *reinterpret_cast<const float4 *>(&Kc[sw128(rx + l16, k)]);
             const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[sw128(ro + l16, k)]);
 #pragma unroll
@@ -552,10 +555,10 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = rx + 4 * lq + i;
-            xr[i] = L.G1[2 * C + r] * (L.V[r * 16 + l16] - L.G1[r] * ak[i]);
+            xr[i] = L.G1[2 * C + r] * (L.V[v_row(r) * 16 + l16] - L.G1[r] * ak[i]);
             ao[i] = L.G1[ro + 4 * lq + i] * aq[i];
         }
-        *reinterpret_cast<float4 *>(&L.X[l16 * AS + rx + 4 * lq]) = make_float4(xr[0], xr[1], xr[2], xr[3]);
+        *reinterpret_cast<float4 *>(&L.X[sw64(l16, rx + 4 * lq)]) = make_float4(xr[0], xr[1], xr[2], xr[3]);
         q35_lds_barrier();                                   /* B1(c) */
 
         /* phase 1b: Delta = T X on rows rx (key blocks 0..w) */
@@ -564,19 +567,19 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= w) {       /* w is wave-uniform: a scalar branch */
                 const float4 ta = *reinterpret_cast<const float4 *>(&L.T[sw64(rx + l16, 16 * blk + 4 * lq)]);
-                const float4 xb = *reinterpret_cast<const float4 *>(&L.X[l16 * AS + 16 * blk + 4 * lq]);
+                const float4 xb = *reinterpret_cast<const float4 *>(&L.X[sw64(l16, 16 * blk + 4 * lq)]);
 #pragma unroll
                 for (int e = 0; e < 4; e++) ad = mfma4(el(ta, e), el(xb, e), ad);
             }
         }
-        *reinterpret_cast<float4 *>(&L.D[l16 * AS + rx + 4 * lq]) = make_float4(ad[0], ad[1], ad[2], ad[3]);
+        *reinterpret_cast<float4 *>(&L.D[sw64(l16, rx + 4 * lq)]) = make_float4(ad[0], ad[1], ad[2], ad[3]);
         q35_lds_barrier();                                   /* B2(c) */
 
         /* phase 2: O += Pm Delta on rows ro (key blocks 0..3-w) */
         float4 db[4];
 #pragma unroll
         for (int blk = 0; blk < 4; blk++)
-            db[blk] = *reinterpret_cast<const float4 *>(&L.D[l16 * AS + 16 * blk + 4 * lq]);
+            db[blk] = *reinterpret_cast<const float4 *>(&L.D[sw64(l16, 16 * blk + 4 * lq)]);
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= 3 - w) {
@@ -607,7 +610,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             const int i0 = 16 * (2 * w + tt);
-            float *sp = &L.S[l16 * XS + i0 + 4 * lq];
+            float *sp = &L.S[sw128(l16, i0 + 4 * lq)];
             const float4 s0 = *reinterpret_cast<const float4 *>(sp);
             f32x4_t acc = {gc * s0.x, gc * s0.y, gc * s0.z, gc * s0.w};
 #pragma unroll
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     for (int u = 0; u < 2; u++) {
         const int idx = u * 256 + t, jj = idx >> 5, i4 = (idx & 31) * 4;
         *reinterpret_cast<float4 *>(state + (size_t)jj * KD + i4) =
-            *reinterpret_cast<const float4 *>(&L.S[jj * XS + i4]);
+            *reinterpret_cast<const float4 *>(&L.S[sw128(jj, i4)]);
     }
 }
 
