@@ -147,3 +147,41 @@ def test_stack_decode_graph_steps_match_oracle(ctx):
          f"{worst_rr[2]:.3e}) delta {worst[1]:.3e} (rel-rms {worst_rr[1]:.3e}); worst state "
          f"rel {worst_state:.3e}; {time.time() - t_start:.1f} s")
     sd.close()
+
+
+def test_stack_start_state_regenerates():
+    """bench.py hands the CPU baseline the stack's starting state after the
+    timed steps, regenerated in place (StackDecode.synth_state): that state
+    must equal the one the steps started from -- the GQA cache rows below
+    ctx, the delta-rule states and the conv ring slots of positions
+    ctx - 3 .. ctx - 1, bit for bit.  (The fourth slot is the one the step
+    at ctx writes before anything reads it, src/attn_qwen.c:480-500.)"""
+    import torch
+
+    from ds4f_hip.stack import StackDecode
+
+    ctx, steps = 4096, 3
+    sd = StackDecode(ctx, steps, seed=0, host_cache=True)
+    cache, kinds = sd.cache, sd.kinds
+    sd.ga.sync(-1, to_host=True, n_kv_tokens=ctx)
+    kv0 = {Lr: cache.kv[Lr, :ctx].copy() for Lr in range(len(kinds)) if kinds[Lr] == 2}
+    lin0, conv0 = cache.lin.copy(), cache.conv.copy()
+    graphs = sd.capture(range(steps))
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    del graphs
+    sd.ga.sync(-1, to_host=True, n_kv_tokens=ctx)
+    moved = any(not np.array_equal(cache.lin[Lr], lin0[Lr]) for Lr in range(len(kinds))
+                if kinds[Lr] != 2)
+    assert moved, "the steps did not advance the delta-rule states"
+    sd.synth_state()
+    sd.ga.sync(-1, to_host=True, n_kv_tokens=ctx)
+    for Lr, kd in enumerate(kinds):
+        if kd == 2:
+            assert np.array_equal(cache.kv[Lr, :ctx], kv0[Lr]), f"layer {Lr} cache rows"
+        else:
+            assert np.array_equal(cache.lin[Lr], lin0[Lr]), f"layer {Lr} state"
+            taps = [(ctx - j) % 4 for j in (3, 2, 1)]
+            assert np.array_equal(cache.conv[Lr][taps], conv0[Lr][taps]), f"layer {Lr} conv ring"
+    sd.close()
