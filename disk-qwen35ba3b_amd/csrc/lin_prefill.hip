@@ -343,10 +343,15 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
 /* ---- 4. sequential scan over chunks per (value head, 16-column block) ---- *
  * With S0 the state block entering the chunk (all 128 key rows, 16 value
  * columns j), per chunk:
- *   phase 1   K S0, Q S0;  X = diag(beta) (V - diag(exp(G)) K S0)
+ *   phase 1   K S0;  X = diag(beta) (V - diag(exp(G)) K S0)
  *   phase 1b  Delta = T X                       (= U - W S0)
  *   phase 2   O = diag(exp(G)) Q S0 + Pm Delta
  *             S_end = exp(G_C) S0 + K^T diag(exp(G_C - G)) Delta
+ * Q S0 is not on the recurrence's path: its operands are read into
+ * registers in phase 1 and its key blocks fill phases 1b and 2 (8 - w and
+ * w of them), so that every wave issues 32, 36 and 48 MFMAs in the three
+ * phases instead of 64 and up to 16 and 48 (one wave at the maximum of
+ * each phase).
  * 8 waves in two roles.  Waves 0-3 compute from LDS only: wave w owns rows
  * 16w.. of X and Delta, rows 16(3-w).. of O (so the causal products are
  * balanced: 116 MFMAs a wave), and key rows 32w..32w+31 of the state
@@ -356,7 +361,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  *   K (double-buffered)          read in 1 and 2, copied for c + 1 in 1 of c
  *   Q, V, exp(G), beta           read in 1,       copied for c + 1 in 1b of c
  *   T                            read in 1b,      copied for c + 1 in 2 of c
- *   Pm, exp(G_C - G), exp(G_C)   read in 2,       copied for c in 1 of c
+ *   Pm, the gate vector again    read in 2,       copied for c in 1 of c
+ *                                (exp(G) for O, exp(G_C - G), exp(G_C))
  * so every copy has at least two phases to land.  K, Q, T and Pm rows sit
  * in LDS with 16-byte granule g of row r at granule g ^ (r % 16) (the
  * copy's lanes fetch the granule their slot holds): the MFMA operand reads
@@ -376,7 +382,7 @@ struct ScanLds {
     float T[C * C];                    /* T [t][s] (sw64) */
     float P[C * C];                    /* Pm [t][s] (sw64); tiles above the diagonal unread */
     float G1[Q35_LIN_GVEC];            /* the chunk's gate vector, for exp(G) and beta (phase 1) */
-    float G2[Q35_LIN_GVEC];            /* the same, for exp(G_C - G) and exp(G_C) (phase 2) */
+    float G2[Q35_LIN_GVEC];            /* the same, for exp(G), exp(G_C - G) and exp(G_C) (phase 2) */
     float S[16 * KD];                  /* state block [j][i] (sw128) */
     float X[16 * C];                   /* X [j][t] (sw64) */
     float D[16 * C];                   /* Delta [j][t] (sw64) */
@@ -536,56 +542,81 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
         const int b0 = c * C, nv = min(C, p.B - b0);
         const float *Kc = L.K[c & 1];
 
-        /* phase 1: K S0 on rows rx, Q S0 on rows ro, over all 128 key rows */
+        /* phase 1: K S0 on rows rx over all 128 key rows; the state block and
+         * the Q rows ro of the 8 key blocks stay in registers for Q S0, which
+         * runs in phases 1b and 2 (blocks 0..7-w and 8-w..7): every wave then
+         * issues 32, 36 and 48 MFMAs in the three phases */
         f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, aq = ak;
+        float4 sbv[8], qav[8];
 #pragma unroll
         for (int blk = 0; blk < 8; blk++) {
             const int k = 16 * blk + 4 * lq;
-            const float4 sb = *reinterpret_cast<const float4 *>(&L.S[sw128(l16, k)]);
+            sbv[blk] = *reinterpret_cast<const float4 *>(&L.S[sw128(l16, k)]);
             const float4 ka = *reinterpret_cast<const float4 *>(&Kc[sw128(rx + l16, k)]);
-            const float4 qa = *reinterpret_cast<const float4 *>(&L.Q[sw128(ro + l16, k)]);
+            qav[blk] = *reinterpret_cast<const float4 *>(&L.Q[sw128(ro + l16, k)]);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                ak = mfma4(el(ka, e), el(sb, e), ak);
-                aq = mfma4(el(qa, e), el(sb, e), aq);
-            }
+            for (int e = 0; e < 4; e++) ak = mfma4(el(ka, e), el(sbv[blk], e), ak);
         }
-        f32x4_t ao;
         float xr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = rx + 4 * lq + i;
             xr[i] = L.G1[2 * C + r] * (L.V[v_row(r) * 16 + l16] - L.G1[r] * ak[i]);
-            ao[i] = L.G1[ro + 4 * lq + i] * aq[i];
         }
         *reinterpret_cast<float4 *>(&L.X[sw64(l16, rx + 4 * lq)]) = make_float4(xr[0], xr[1], xr[2], xr[3]);
         q35_lds_barrier();                                   /* B1(c) */
 
-        /* phase 1b: Delta = T X on rows rx (key blocks 0..w) */
+        /* phase 1b: Q S0 blocks 0..7-w from registers (under the T and X
+         * reads), then Delta = T X on rows rx (key blocks 0..w) */
         f32x4_t ad = {0.f, 0.f, 0.f, 0.f};
+        float4 ta[4], xb[4];
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= w) {       /* w is wave-uniform: a scalar branch */
-                const float4 ta = *reinterpret_cast<const float4 *>(&L.T[sw64(rx + l16, 16 * blk + 4 * lq)]);
-                const float4 xb = *reinterpret_cast<const float4 *>(&L.X[sw64(l16, 16 * blk + 4 * lq)]);
+                ta[blk] = *reinterpret_cast<const float4 *>(&L.T[sw64(rx + l16, 16 * blk + 4 * lq)]);
+                xb[blk] = *reinterpret_cast<const float4 *>(&L.X[sw64(l16, 16 * blk + 4 * lq)]);
+            }
+        }
 #pragma unroll
-                for (int e = 0; e < 4; e++) ad = mfma4(el(ta, e), el(xb, e), ad);
+        for (int blk = 0; blk < 8; blk++) {
+            if (blk <= 7 - w) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) aq = mfma4(el(qav[blk], e), el(sbv[blk], e), aq);
+            }
+        }
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) {
+            if (blk <= w) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) ad = mfma4(el(ta[blk], e), el(xb[blk], e), ad);
             }
         }
         *reinterpret_cast<float4 *>(&L.D[sw64(l16, rx + 4 * lq)]) = make_float4(ad[0], ad[1], ad[2], ad[3]);
         q35_lds_barrier();                                   /* B2(c) */
 
-        /* phase 2: O += Pm Delta on rows ro (key blocks 0..3-w) */
-        float4 db[4];
+        /* phase 2: Q S0 blocks 8-w..7, then O = exp(G) Q S0 + Pm Delta on
+         * rows ro (key blocks 0..3-w); exp(G) from the phase-2 gate copy */
+        float4 db[4], pa[4];
 #pragma unroll
-        for (int blk = 0; blk < 4; blk++)
+        for (int blk = 0; blk < 4; blk++) {
             db[blk] = *reinterpret_cast<const float4 *>(&L.D[sw64(l16, 16 * blk + 4 * lq)]);
+            if (blk <= 3 - w)
+                pa[blk] = *reinterpret_cast<const float4 *>(&L.P[sw64(ro + l16, 16 * blk + 4 * lq)]);
+        }
+        const float4 eg = *reinterpret_cast<const float4 *>(&L.G2[ro + 4 * lq]);
+#pragma unroll
+        for (int blk = 0; blk < 8; blk++) {
+            if (blk > 7 - w) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) aq = mfma4(el(qav[blk], e), el(sbv[blk], e), aq);
+            }
+        }
+        f32x4_t ao = {eg.x * aq[0], eg.y * aq[1], eg.z * aq[2], eg.w * aq[3]};
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= 3 - w) {
-                const float4 pa = *reinterpret_cast<const float4 *>(&L.P[sw64(ro + l16, 16 * blk + 4 * lq)]);
 #pragma unroll
-                for (int e = 0; e < 4; e++) ao = mfma4(el(pa, e), el(db[blk], e), ao);
+                for (int e = 0; e < 4; e++) ao = mfma4(el(pa[blk], e), el(db[blk], e), ao);
             }
         }
         {
