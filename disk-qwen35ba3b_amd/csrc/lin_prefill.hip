@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  * block.  Waves 4-7 copy the operands global -> LDS with direct-to-LDS
  * buffer loads (no register staging), each into the tile's LDS image, and
  * count their own loads (vmcnt) before the barrier that publishes a tile:
- *   K (double-buffered)          read in 1 and 2, copied for c + 1 in 1 of c
+ *   K (double-buffered)          read in 1 and 2, copied for c + 1 in 1b of c
  *   Q, V, exp(G), beta           read in 1,       copied for c + 1 in 1b of c
  *   T                            read in 1b,      copied for c + 1 in 2 of c
  *   Pm, the gate vector again    read in 2,       copied for c in 1 of c
@@ -478,8 +478,9 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     float *state = p.state + ((size_t)g.h * VD + 16 * g.jb) * KD;
 
     if (wave >= 4) {
-        /* ---- copy waves: loads counted per wave (13 in step 1, 10 in
-         * step 2, 4 in step 3 of every chunk) ---- */
+        /* ---- copy waves: loads counted per wave (5 in step 1, 18 in
+         * step 2, 4 in step 3 of every chunk; phase 1, whose operand reads
+         * are the heaviest, carries the fewest LDS writes) ---- */
         ScanCopy cp;
         cp.post = p.post;
         cp.T = p.T;
@@ -505,15 +506,15 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
         q35_lds_barrier();                                   /* B0 */
         for (int c = 0; c <= last; c++) {
             const int c1 = min(c + 1, last);
-            /* step 1 (phase 1 of c): Pm and gates of c, K of c + 1 into the
-             * buffer phase 2 of c - 1 read (on the last chunk, a copy nobody
-             * reads, which keeps the load counts the same) */
+            /* step 1 (phase 1 of c): Pm and gates of c */
             cp.pm(c);
             cp.gv(cp.lG2, c);
-            cp.k(c1, (c + 1) & 1);
-            q35_wait_vm<13>();                               /* T of c has landed */
+            q35_wait_vm<5>();                                /* T of c has landed */
             q35_lds_barrier();                               /* B1(c) */
-            /* step 2 (phase 1b of c): Q, V, gates of c + 1 */
+            /* step 2 (phase 1b of c): K of c + 1 into the buffer phase 2 of
+             * c - 1 read (on the last chunk, a copy nobody reads, which keeps
+             * the load counts the same), Q, V, gates of c + 1 */
+            cp.k(c1, (c + 1) & 1);
             cp.q(c1);
             cp.v(c1);
             cp.gv(cp.lG1, c1);
