@@ -358,12 +358,17 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  * block.  Waves 4-7 copy the operands global -> LDS with direct-to-LDS
  * buffer loads (no register staging), each into the tile's LDS image, and
  * count their own loads (vmcnt) before the barrier that publishes a tile:
- *   K (double-buffered)          read in 1 and 2, copied for c + 1 in 1b of c
- *   Q, V, exp(G), beta           read in 1,       copied for c + 1 in 1b of c
+ *   K (double-buffered)          read in 1 and 2, copied for c + 1 in 1 of c
+ *   Pm (double-buffered)         read in 2,       copied for c + 1 in 1 of c
+ *   gates (double-buffered)      read in 1 and 2, copied for c + 1 in 1 of c
+ *   Q, V                         read in 1,       copied for c + 1 in 1b of c
  *   T                            read in 1b,      copied for c + 1 in 2 of c
- *   Pm, the gate vector again    read in 2,       copied for c in 1 of c
- *                                (exp(G) for O, exp(G_C - G), exp(G_C))
- * so every copy has at least two phases to land.  K, Q, T and Pm rows sit
+ * so every copy has at least two phases to land, and no barrier waits for
+ * a copy wave still issuing: each 1 KB load instruction passes the
+ * texture addresser in about 16 cycles, and the 18 a wave issued in phase
+ * 1b (72 a CU) held the barrier after it about 500 cycles.  T and Pm hold
+ * only their 10 lower 16x16 blocks, which frees the LDS for the second Pm
+ * buffer.  K, Q, T and Pm rows sit
  * in LDS with 16-byte granule g of row r at granule g ^ (r % 16) (the
  * copy's lanes fetch the granule their slot holds): the MFMA operand reads
  * of 16 consecutive rows hit 16 distinct bank groups.  Workgroups are dealt
@@ -379,10 +384,9 @@ struct ScanLds {
     float K[2][C * KD];                /* K rows [t][i], chunk c in K[c & 1] (sw128) */
     float Q[C * KD];                   /* Q rows [t][i] (sw128) */
     float V[C * 16];                   /* V slice [t][j] */
-    float T[C * C];                    /* T [t][s] (sw64) */
-    float P[C * C];                    /* Pm [t][s] (sw64); tiles above the diagonal unread */
-    float G1[Q35_LIN_GVEC];            /* the chunk's gate vector, for exp(G) and beta (phase 1) */
-    float G2[Q35_LIN_GVEC];            /* the same, for exp(G), exp(G_C - G) and exp(G_C) (phase 2) */
+    float T[10 * 256];                 /* the 10 lower 16x16 blocks of T (tri_off) */
+    float P[2][10 * 256];              /* the same of Pm, chunk c in P[c & 1] */
+    float G[2][Q35_LIN_GVEC];          /* gate vectors, chunk c in G[c & 1] */
     float S[16 * KD];                  /* state block [j][i] (sw128) */
     float X[16 * C];                   /* X [j][t] (sw64) */
     float D[16 * C];                   /* Delta [j][t] (sw64) */
@@ -393,6 +397,13 @@ static_assert(Q35_LIN_GVEC == 256, "a gate vector is four 64-float quarters, one
  * so the X update's reads of rows r and r + 4 (one 32-lane half of a wave)
  * fall in the two different 16-bank halves (the map is its own inverse) */
 __device__ __forceinline__ int v_row(int t) { return t ^ ((t >> 2) & 1); }
+
+/* The 10 16x16 blocks (a, b), b <= a, of a 64x64 lower triangle: block
+ * a (a + 1) / 2 + b at 256 floats each, row r of a block 16 floats, its
+ * 16-byte granule g at g ^ ((r >> 2) & 3), so an operand read of the 16
+ * rows of one granule column covers all 64 banks */
+__host__ __device__ constexpr int tri_idx(int a, int b) { return a * (a + 1) / 2 + b; }
+__device__ __forceinline__ int tri_off(int j, int r, int gr) { return j * 256 + r * 16 + 4 * (gr ^ ((r >> 2) & 3)); }
 
 struct ScanGeo {
     int h, jb, kh, VH, KH, rows;
@@ -410,7 +421,7 @@ struct ScanCopy {
     int B;
     ScanGeo g;
     int dw, lane;
-    uint32_t lK, lQ, lV, lT, lP, lG1, lG2;      /* LDS byte addresses (lK: K[0]; K[1] follows) */
+    uint32_t lK, lQ, lV, lT, lP, lG;            /* LDS byte addresses (K[0], P[0], G[0]; [1] follows) */
 
     /* 8 copies of a [64][128] row tile (K or Q rows, channels ch0 ..) */
     /* the post rows of chunk c (rows at and past the batch end read as zero) */
@@ -418,10 +429,11 @@ struct ScanCopy {
         const int b0 = c * C, nv = min(C, B - b0);
         return blk_rsrc(q35_uniform_ptr(post + (size_t)b0 * g.rows), (size_t)nv * g.rows);
     }
+    template <int I0 = 0, int I1 = 8>
     __device__ __forceinline__ void rows128(uint32_t lds, int c, int ch0) const {
         const __amdgpu_buffer_rsrc_t rs = rows(c);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = I0; i < I1; i++) {
             const int d = dw + 4 * i, r = 2 * d + (lane >> 5), gr = (lane & 31) ^ (r & 15);
             q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * d),
                       (uint32_t)((r * g.rows + ch0 + 4 * gr) * 4), 0);
@@ -429,6 +441,11 @@ struct ScanCopy {
     }
     /* K rows of chunk c into K[buf] */
     __device__ __forceinline__ void k(int c, int buf) const { rows128(lK + buf * C * KD * 4, c, (g.KH + g.kh) * KD); }
+    /* the first or second half of those copies */
+    template <int H>
+    __device__ __forceinline__ void k_half(int c, int buf) const {
+        rows128<4 * H, 4 * H + 4>(lK + buf * C * KD * 4, c, (g.KH + g.kh) * KD);
+    }
     __device__ __forceinline__ void q(int c) const { rows128(lQ, c, g.kh * KD); }
     /* one copy of the V slice (16 rows of 16 floats) */
     __device__ __forceinline__ void v(int c) const {
@@ -437,18 +454,25 @@ struct ScanCopy {
         q35_dma16(rs, __builtin_amdgcn_readfirstlane(lV + 1024 * dw),
                   (uint32_t)((r * g.rows + 2 * g.KH * KD + g.h * VD + 16 * g.jb + 4 * (lane & 3)) * 4), 0);
     }
-    /* 4 copies of a [64][64] tile of chunk c's T or Pm */
-    __device__ __forceinline__ void tile64(uint32_t lds, const float *base, int c) const {
+    /* 3 of the 10 lower 16x16 blocks of chunk c's T or Pm [64][64] (blocks
+     * dw, dw + 4, dw + 8, the last block again past 9: copy waves 2 and 3
+     * write block 9 a second and third time, the same bytes, so every wave
+     * counts 3 loads); lane l -> bytes 16 l of the block: row l / 4, stored
+     * granule l % 4 */
+    __device__ __forceinline__ void tri(uint32_t lds, const float *base, int c) const {
         const size_t ch = (size_t)c * g.VH + g.h;
         const __amdgpu_buffer_rsrc_t rs = blk_rsrc(q35_uniform_ptr(base + ch * C * C), C * C);
+        const int r = lane >> 2, gr = (lane & 3) ^ ((r >> 2) & 3);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int d = dw + 4 * i, r = 4 * d + (lane >> 4), gr = (lane & 15) ^ (r & 15);
-            q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * d), (uint32_t)((r * C + 4 * gr) * 4), 0);
+        for (int i = 0; i < 3; i++) {
+            const int j = min(dw + 4 * i, 9);
+            const int a = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, b = j - tri_idx(a, 0);
+            q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * j),
+                      (uint32_t)(((16 * a + r) * C + 16 * b + 4 * gr) * 4), 0);
         }
     }
-    __device__ __forceinline__ void t(int c) const { tile64(lT, T, c); }
-    __device__ __forceinline__ void pm(int c) const { tile64(lP, Pm, c); }
+    __device__ __forceinline__ void t(int c) const { tri(lT, T, c); }
+    __device__ __forceinline__ void pm(int c, int buf) const { tri(lP + buf * 10 * 1024, Pm, c); }
     /* a quarter of chunk c's gate vector */
     __device__ __forceinline__ void gv(uint32_t lds, int c) const {
         const size_t ch = (size_t)c * g.VH + g.h;
@@ -473,7 +497,7 @@ __device__ __forceinline__ void scan_chunks(ScanLds &L, const Q35LinPrefill &p, 
     const int l16 = lane & 15, lq = lane >> 4;
     for (int c = 0; c <= last; c++) {
         const int b0 = c * C, nv = min(C, p.B - b0);
-        const float *Kc = L.K[c & 1];
+        const float *Kc = L.K[c & 1], *Gc = L.G[c & 1], *Pc = L.P[c & 1];
 
         /* phase 1: K S0 on rows rx over all 128 key rows; the state block and
          * the Q rows ro of the 8 key blocks stay in registers for Q S0, which
@@ -494,7 +518,7 @@ __device__ __forceinline__ void scan_chunks(ScanLds &L, const Q35LinPrefill &p, 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = rx + 4 * lq + i;
-            xr[i] = L.G1[2 * C + r] * (L.V[v_row(r) * 16 + l16] - L.G1[r] * ak[i]);
+            xr[i] = Gc[2 * C + r] * (L.V[v_row(r) * 16 + l16] - Gc[r] * ak[i]);
         }
         *reinterpret_cast<float4 *>(&L.X[sw64(l16, rx + 4 * lq)]) = make_float4(xr[0], xr[1], xr[2], xr[3]);
         q35_lds_barrier();                                   /* B1(c) */
@@ -507,7 +531,7 @@ __device__ __forceinline__ void scan_chunks(ScanLds &L, const Q35LinPrefill &p, 
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
             if (blk <= w) {       /* compile-time in each instance */
-                ta[blk] = *reinterpret_cast<const float4 *>(&L.T[sw64(rx + l16, 16 * blk + 4 * lq)]);
+                ta[blk] = *reinterpret_cast<const float4 *>(&L.T[tri_off(tri_idx(w, blk), l16, lq)]);
                 xb[blk] = *reinterpret_cast<const float4 *>(&L.X[sw64(l16, 16 * blk + 4 * lq)]);
             }
         }
@@ -536,9 +560,9 @@ __device__ __forceinline__ void scan_chunks(ScanLds &L, const Q35LinPrefill &p, 
         for (int blk = 0; blk < 4; blk++) {
             db[blk] = *reinterpret_cast<const float4 *>(&L.D[sw64(l16, 16 * blk + 4 * lq)]);
             if (blk <= 3 - w)
-                pa[blk] = *reinterpret_cast<const float4 *>(&L.P[sw64(ro + l16, 16 * blk + 4 * lq)]);
+                pa[blk] = *reinterpret_cast<const float4 *>(&Pc[tri_off(tri_idx(3 - w, blk), l16, lq)]);
         }
-        const float4 eg = *reinterpret_cast<const float4 *>(&L.G2[ro + 4 * lq]);
+        const float4 eg = *reinterpret_cast<const float4 *>(&Gc[ro + 4 * lq]);
 #pragma unroll
         for (int blk = 0; blk < 8; blk++) {
             if (blk > 7 - w) {
@@ -566,13 +590,13 @@ __device__ __forceinline__ void scan_chunks(ScanLds &L, const Q35LinPrefill &p, 
          * and MFMA), B = exp(G_C - G_s) Delta */
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) {
-            const float4 gk = *reinterpret_cast<const float4 *>(&L.G2[C + 16 * blk + 4 * lq]);
+            const float4 gk = *reinterpret_cast<const float4 *>(&Gc[C + 16 * blk + 4 * lq]);
             db[blk].x *= gk.x;
             db[blk].y *= gk.y;
             db[blk].z *= gk.z;
             db[blk].w *= gk.w;
         }
-        const float gc = L.G2[3 * C];
+        const float gc = Gc[3 * C];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             const int i0 = 16 * (2 * w + tt);
@@ -611,9 +635,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
     float *state = p.state + ((size_t)g.h * VD + 16 * g.jb) * KD;
 
     if (wave >= 4) {
-        /* ---- copy waves: loads counted per wave (5 in step 1, 18 in
-         * step 2, 4 in step 3 of every chunk; phase 1, whose operand reads
-         * are the heaviest, carries the fewest LDS writes) ---- */
+        /* ---- copy waves: loads counted per wave (12 in step 1, 9 in
+         * step 2, 3 in step 3 of every chunk) ---- */
         ScanCopy cp;
         cp.post = p.post;
         cp.T = p.T;
@@ -627,35 +650,32 @@ __global__ __launch_bounds__(SCAN_THREADS) void scan_kernel(Q35LinPrefill p) {
         cp.lQ = q35_lds_addr(L.Q);
         cp.lV = q35_lds_addr(L.V);
         cp.lT = q35_lds_addr(L.T);
-        cp.lP = q35_lds_addr(L.P);
-        cp.lG1 = q35_lds_addr(L.G1);
-        cp.lG2 = q35_lds_addr(L.G2);
+        cp.lP = q35_lds_addr(L.P[0]);
+        cp.lG = q35_lds_addr(L.G[0]);
         cp.k(0, 0);
         cp.q(0);
         cp.v(0);
-        cp.gv(cp.lG1, 0);
+        cp.gv(cp.lG, 0);
         cp.t(0);
+        cp.pm(0, 0);
         q35_wait_vm<0>();
         q35_lds_barrier();                                   /* B0 */
         for (int c = 0; c <= last; c++) {
             const int c1 = min(c + 1, last);
-            /* step 1 (phase 1 of c): Pm and gates of c */
-            cp.pm(c);
-            cp.gv(cp.lG2, c);
-            q35_wait_vm<5>();                                /* T of c has landed */
-            q35_lds_barrier();                               /* B1(c) */
-            /* step 2 (phase 1b of c): K of c + 1 into the buffer phase 2 of
-             * c - 1 read (on the last chunk, a copy nobody reads, which keeps
-             * the load counts the same), Q, V, gates of c + 1 */
+            /* step 1 (phase 1 of c): K, Pm and gates of c + 1, each into
+             * the buffer phase 2 of c - 1 read */
             cp.k(c1, (c + 1) & 1);
+            cp.pm(c1, (c + 1) & 1);
+            cp.gv(cp.lG + ((c + 1) & 1) * 1024, c1);
+            q35_wait_vm<12>();                               /* T of c (and Pm of c) */
+            q35_lds_barrier();                               /* B1(c) */
+            /* step 2 (phase 1b of c): Q, V of c + 1 */
             cp.q(c1);
             cp.v(c1);
-            cp.gv(cp.lG1, c1);
-            q35_wait_vm<18>();                               /* Pm and gates of c */
             q35_lds_barrier();                               /* B2(c) */
             /* step 3 (phase 2 of c): T of c + 1 */
             cp.t(c1);
-            q35_wait_vm<4>();                                /* K, Q, V, gates of c + 1 */
+            q35_wait_vm<3>();                                /* K, Pm, gates, Q, V of c + 1 */
             q35_lds_barrier();                               /* B3(c) */
         }
         q35_wait_vm<0>();
