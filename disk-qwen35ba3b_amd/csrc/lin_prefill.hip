@@ -133,6 +133,14 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
 __device__ __forceinline__ int sw128(int r, int k) { return r * KD + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
 __device__ __forceinline__ int sw64(int r, int k) { return r * C + ((((k >> 2) ^ (r & 15))) << 2) + (k & 3); }
 
+/* T and Pm leave the chunk kernel as the 10 16x16 blocks (a, b), b <= a, of a 64x64 lower triangle: block
+ * a (a + 1) / 2 + b at 256 floats each, row r of a block 16 floats (the
+ * scan's LDS image of a block holds its 16-byte granule g of row r at
+ * g ^ ((r >> 2) & 3), so an operand read of the 16 rows of one granule
+ * column covers all 64 banks) */
+__host__ __device__ constexpr int tri_idx(int a, int b) { return a * (a + 1) / 2 + b; }
+__device__ __forceinline__ int tri_off(int j, int r, int gr) { return j * 256 + r * 16 + 4 * (gr ^ ((r >> 2) & 3)); }
+
 /* 16x16 blocks of a 64x64 triangle: index of block (a, c), a <= c, among the
  * 10 blocks on and above the diagonal */
 __device__ __forceinline__ int blk_q(int a, int c) { return a * (9 - a) / 2 + (c - a); }
@@ -140,9 +148,9 @@ constexpr int BS = 20, BLK = 16 * BS;
 
 /* ---- 3. per (chunk, key head): decay vectors, Pm and T = (I + A)^-1 ------ *
  * The two value heads 2kh, 2kh+1 of key head kh share K K^T and Q K^T; they
- * differ in the gates.  Outputs per (chunk, value head): gvec, Pm (tiles on
- * and below the diagonal) and T [64][64] (lower triangular, unit diagonal,
- * zeros above). */
+ * differ in the gates.  Outputs per (chunk, value head): gvec, and Pm and
+ * T (lower triangular, unit diagonal) as their 10 blocks on and below the
+ * diagonal, 1 KB each (tri_idx), in a [64][64]-sized slot. */
 __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     const int c = blockIdx.x, kh = blockIdx.y;
     const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
@@ -263,9 +271,9 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
                 *reinterpret_cast<float4 *>(&MB[(v * 10 + blk_q(tc, tr)) * BLK + l16 * BS + 4 * lq]) =
                     make_float4(o[0], o[1], o[2], o[3]);
             } else {
-                float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C;
+                float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C + tri_idx(tr, tc) * 256;
 #pragma unroll
-                for (int i = 0; i < 4; i++) Pm[(16 * tr + 4 * lq + i) * C + s] = o[i];
+                for (int i = 0; i < 4; i++) Pm[(4 * lq + i) * 16 + l16] = o[i];
             }
         }
     }
@@ -327,16 +335,15 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
         q35_lds_barrier();
     }
 
-    /* T rows out: 2 heads x 64 rows x 16 float4; blocks above the diagonal
-     * are zero */
+    /* T out: 2 heads x the 10 lower blocks x 16 rows x 4 float4, each wave
+     * instruction one whole 1 KB block */
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int idx = u * 256 + t, v = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
-        const int bb = r >> 4, ba = c4 >> 4;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (bb >= ba)
-            o = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(ba, bb)) * BLK + (r & 15) * BS + (c4 & 15)]);
-        *reinterpret_cast<float4 *>(p.T + ((size_t)c * VH + 2 * kh + v) * C * C + r * C + c4) = o;
+    for (int u = 0; u < 5; u++) {
+        const int idx = u * 256 + t, v = idx / 640, rem = idx % 640;
+        const int j = rem >> 6, r = (rem >> 2) & 15, q4 = rem & 3;
+        const int bb = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, ba = j - tri_idx(bb, 0);
+        const float4 o = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(ba, bb)) * BLK + r * BS + 4 * q4]);
+        *reinterpret_cast<float4 *>(p.T + ((size_t)c * VH + 2 * kh + v) * C * C + j * 256 + r * 16 + 4 * q4) = o;
     }
 }
 
@@ -398,12 +405,6 @@ static_assert(Q35_LIN_GVEC == 256, "a gate vector is four 64-float quarters, one
  * fall in the two different 16-bank halves (the map is its own inverse) */
 __device__ __forceinline__ int v_row(int t) { return t ^ ((t >> 2) & 1); }
 
-/* The 10 16x16 blocks (a, b), b <= a, of a 64x64 lower triangle: block
- * a (a + 1) / 2 + b at 256 floats each, row r of a block 16 floats, its
- * 16-byte granule g at g ^ ((r >> 2) & 3), so an operand read of the 16
- * rows of one granule column covers all 64 banks */
-__host__ __device__ constexpr int tri_idx(int a, int b) { return a * (a + 1) / 2 + b; }
-__device__ __forceinline__ int tri_off(int j, int r, int gr) { return j * 256 + r * 16 + 4 * (gr ^ ((r >> 2) & 3)); }
 
 struct ScanGeo {
     int h, jb, kh, VH, KH, rows;
@@ -454,11 +455,11 @@ struct ScanCopy {
         q35_dma16(rs, __builtin_amdgcn_readfirstlane(lV + 1024 * dw),
                   (uint32_t)((r * g.rows + 2 * g.KH * KD + g.h * VD + 16 * g.jb + 4 * (lane & 3)) * 4), 0);
     }
-    /* 3 of the 10 lower 16x16 blocks of chunk c's T or Pm [64][64] (blocks
-     * dw, dw + 4, dw + 8, the last block again past 9: copy waves 2 and 3
-     * write block 9 a second and third time, the same bytes, so every wave
-     * counts 3 loads); lane l -> bytes 16 l of the block: row l / 4, stored
-     * granule l % 4 */
+    /* 3 of the 10 blocks of chunk c's T or Pm (blocks dw, dw + 4, dw + 8,
+     * the last block again past 9: copy waves 2 and 3 write block 9 a
+     * second and third time, the same bytes, so every wave counts 3 loads),
+     * each 1 KB contiguous in memory; lane l -> bytes 16 l of the block's
+     * LDS image: row l / 4, stored granule l % 4 */
     __device__ __forceinline__ void tri(uint32_t lds, const float *base, int c) const {
         const size_t ch = (size_t)c * g.VH + g.h;
         const __amdgpu_buffer_rsrc_t rs = blk_rsrc(q35_uniform_ptr(base + ch * C * C), C * C);
@@ -466,9 +467,7 @@ struct ScanCopy {
 #pragma unroll
         for (int i = 0; i < 3; i++) {
             const int j = min(dw + 4 * i, 9);
-            const int a = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, b = j - tri_idx(a, 0);
-            q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * j),
-                      (uint32_t)(((16 * a + r) * C + 16 * b + 4 * gr) * 4), 0);
+            q35_dma16(rs, __builtin_amdgcn_readfirstlane(lds + 1024 * j), (uint32_t)((j * 256 + r * 16 + 4 * gr) * 4), 0);
         }
     }
     __device__ __forceinline__ void t(int c) const { tri(lT, T, c); }
