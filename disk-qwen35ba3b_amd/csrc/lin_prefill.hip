@@ -370,15 +370,15 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
  *   gates (double-buffered)      read in 1 and 2, copied for c + 1 in 1 of c
  *   Q, V                         read in 1,       copied for c + 1 in 1b of c
  *   T                            read in 1b,      copied for c + 1 in 2 of c
- * so every copy has at least two phases to land, and no barrier waits for
- * a copy wave still issuing: each 1 KB load instruction passes the
- * texture addresser in about 16 cycles, and the 18 a wave issued in phase
- * 1b (72 a CU) held the barrier after it about 500 cycles.  T and Pm hold
- * only their 10 lower 16x16 blocks, which frees the LDS for the second Pm
- * buffer.  K, Q, T and Pm rows sit
- * in LDS with 16-byte granule g of row r at granule g ^ (r % 16) (the
- * copy's lanes fetch the granule their slot holds): the MFMA operand reads
- * of 16 consecutive rows hit 16 distinct bank groups.  Workgroups are dealt
+ * so every copy has at least two phases to land, and the loads are spread
+ * over the phases: a copy wave reaches a barrier only once it has issued
+ * its loads, and the 18 a wave once issued in phase 1b (72 a CU) held the
+ * barrier after it about 500 cycles.  T and Pm hold only their 10 lower
+ * 16x16 blocks (tri_off), which frees the LDS for the second Pm buffer.
+ * K and Q rows sit in LDS with 16-byte granule g of row r at granule
+ * g ^ (r % 16) (the copy's lanes fetch the granule their slot holds), as do
+ * the state block, X and Delta: the MFMA operand reads of 16 consecutive
+ * rows hit 16 distinct bank groups.  Workgroups are dealt
  * round-robin over the 8 XCDs (id mod 8): with 8 | key heads, workgroup n
  * runs key head (n & 7) + 8 (n >> 7), its value head (n >> 6) & 1 and
  * block (n >> 3) & 7, so the 16 workgroups of a key head (both value
@@ -404,7 +404,6 @@ static_assert(Q35_LIN_GVEC == 256, "a gate vector is four 64-float quarters, one
  * so the X update's reads of rows r and r + 4 (one 32-lane half of a wave)
  * fall in the two different 16-bank halves (the map is its own inverse) */
 __device__ __forceinline__ int v_row(int t) { return t ^ ((t >> 2) & 1); }
-
 
 struct ScanGeo {
     int h, jb, kh, VH, KH, rows;
