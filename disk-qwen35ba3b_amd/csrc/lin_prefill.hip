@@ -23,7 +23,7 @@
  *   conv_kernel  per token: conv1d + SiLU (ring taps for positions before
  *                t0), q/k RMS-normalisation, gates -> post [B][rows] (the
  *                reference's mutated qkv) and gates [B][VH][2]
- *   chunk_kernel per (chunk, key head), all in parallel: K K^T and Q K^T
+ *   chunk_kernel per (chunk, key head), strided over 512 workgroups: K K^T and Q K^T
  *                on fp32 MFMA (shared by the key head's two value heads),
  *                then per value head A, Pm, the decay vectors and T by
  *                16x16 blocks (diagonal blocks by back substitution, the
@@ -150,26 +150,40 @@ constexpr int BS = 20, BLK = 16 * BS;
  * The two value heads 2kh, 2kh+1 of key head kh share K K^T and Q K^T; they
  * differ in the gates.  Outputs per (chunk, value head): gvec, and Pm and
  * T (lower triangular, unit diagonal) as their 10 blocks on and below the
- * diagonal, 1 KB each (tri_idx), in a [64][64]-sized slot. */
-__global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
-    const int c = blockIdx.x, kh = blockIdx.y;
-    const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
-    const int l16 = lane & 15, lq = lane >> 4;
+ * diagonal, 1 KB each (tri_idx), in a [64][64]-sized slot.
+ * Items (chunk, key head) = (it % n_chunks, it / n_chunks) are strided over
+ * at most CHUNK_GRID workgroups (two a CU): a workgroup requests the next
+ * item's K and Q rows into registers as soon as the current item's rows are
+ * in LDS, so they stream in under the current item's MFMA phases instead of
+ * every workgroup of a second round loading at once. */
+constexpr int CHUNK_GRID = 512;
+
+/* thread t's 16 float4s of an item's K and Q rows: float4 u * 256 + t is
+ * row idx >> 5, columns 4 (idx & 31) ..; raw buffer loads over the chunk's
+ * rows, so rows past the batch end read as zero */
+struct ChunkRows {
+    float4 k[8], q[8];
+};
+__device__ __forceinline__ void chunk_rows_load(ChunkRows &R, const Q35LinPrefill &p, int it, int rows) {
+    const int c = it % p.n_chunks, kh = it / p.n_chunks;
+    const int b0 = c * C, nv = min(C, p.B - b0);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<float *>(p.post) + (size_t)b0 * rows), 0, nv * rows * 4, Q35_BUF_DW3);
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int idx = u * 256 + t, r = idx >> 5, c4 = (idx & 31) * 4;
+        const int ok = (r * rows + (p.k_heads + kh) * KD + c4) * 4, oq = (r * rows + kh * KD + c4) * 4;
+        R.k[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok, 0, 0));
+        R.q[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, oq, 0, 0));
+    }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(Q35LinPrefill p) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
-    const int b0 = c * C, nv = min(C, p.B - b0);
-
-    /* the conv ring: slot pos % 4 <- raw row of pos for the last min(B, 4)
-     * tokens, written by the last chunk's workgroups (the conv kernel, which
-     * reads the ring, has finished) */
-    if (c == p.n_chunks - 1) {
-        const int nr = min(p.B, 4), n4 = rows / 4;
-        for (int i = kh * 256 + t; i < nr * n4; i += KH * 256) {
-            const int b = p.B - nr + i / n4, c4 = 4 * (i % n4);
-            *reinterpret_cast<float4 *>(p.ring + (size_t)((p.t0 + b) & 3) * rows + c4) =
-                *reinterpret_cast<const float4 *>(p.qkv + (size_t)b * rows + c4);
-        }
-    }
+    const int n_items = p.n_chunks * KH;
 
     /* K and Q rows, later A^T of both value heads, later T of both */
     __shared__ __align__(16) float sbuf[2 * C * KD];
@@ -177,173 +191,195 @@ __global__ __launch_bounds__(256) void chunk_kernel(Q35LinPrefill p) {
     __shared__ double sG[2][C];
     __shared__ float sBeta[2][C];
 
-    /* gates and the chunk-local cumulative log-decay of value head 2kh + w
-     * (pads: g = beta = 0) */
-    if (w < 2) {
-        const int h = 2 * kh + w;
-        float g = 0.f, beta = 0.f;
-        if (lane < nv) {
-            const float2 gb = *reinterpret_cast<const float2 *>(p.gates + ((size_t)(b0 + lane) * VH + h) * 2);
-            g = gb.x;
-            beta = gb.y;
-        }
-        double G = g;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const double o = __shfl_up(G, off);
-            if (lane >= off) G += o;
-        }
-        sG[w][lane] = G;
-        sBeta[w][lane] = beta;
-        const double Gc = __shfl(G, 63);
-        float *gv = p.gvec + ((size_t)c * VH + h) * Q35_LIN_GVEC;
-        gv[lane] = (float)exp(G);
-        gv[C + lane] = (float)exp(Gc - G);
-        gv[2 * C + lane] = beta;
-        if (lane == 0) gv[3 * C] = (float)exp(Gc);
-    }
-    /* K and Q rows of the chunk into LDS; pad rows zero */
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int idx = u * 256 + t, r = idx >> 5, c4 = (idx & 31) * 4;
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), qv = kv;
-        if (r < nv) {
-            const float *row = p.post + (size_t)(b0 + r) * rows;
-            kv = *reinterpret_cast<const float4 *>(row + KH * KD + kh * KD + c4);
-            qv = *reinterpret_cast<const float4 *>(row + kh * KD + c4);
-        }
-        *reinterpret_cast<float4 *>(&sK[sw128(r, c4)]) = kv;
-        *reinterpret_cast<float4 *>(&sQ[sw128(r, c4)]) = qv;
-    }
-    q35_lds_barrier();
+    ChunkRows R;
+    chunk_rows_load(R, p, blockIdx.x, rows);
+    for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+        /* the thread index as an opaque value per item: the LDS addresses
+         * derived from it are then computed where they are used, not hoisted
+         * out of the item loop into registers held across it */
+        int t = threadIdx.x;
+        asm volatile("" : "+v"(t));
+        const int lane = t & 63, l16 = lane & 15, lq = lane >> 4;
+        const int c = it % p.n_chunks, kh = it / p.n_chunks;
+        const int b0 = c * C, nv = min(C, p.B - b0);
 
-    /* K K^T and Q K^T, the 10 lower 16x16 tiles of each: tile n (0..19),
-     * wave w takes n = w, w+4, ..., w+16.  Lane l holds rows 4*(l/16)+i. */
-    f32x4_t res[5];
-#pragma unroll
-    for (int k = 0; k < 5; k++) {
-        const int n = w + 4 * k, m = n % 10;
-        const int tr = m < 1 ? 0 : m < 3 ? 1 : m < 6 ? 2 : 3;
-        const int tc = m - (tr * (tr + 1)) / 2;
-        const float *X = n < 10 ? sK : sQ;
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int blk = 0; blk < KD / 16; blk++) {
-            const float4 xa = *reinterpret_cast<const float4 *>(&X[sw128(16 * tr + l16, 16 * blk + 4 * lq)]);
-            const float4 yb = *reinterpret_cast<const float4 *>(&sK[sw128(16 * tc + l16, 16 * blk + 4 * lq)]);
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc = mfma4(el(xa, e), el(yb, e), acc);
-        }
-        res[k] = acc;
-    }
-    q35_lds_barrier();                       /* K and Q no longer read */
-
-    /* T = (I + A)^-1 in 16x16 blocks.  With M = A^T (strictly upper,
-     * M[s][r] = A[r][s]) and U = (I + M)^-1 = T^T, for blocks a <= b:
-     *   U_aa = (I + M_aa)^-1                      (back substitution)
-     *   U_ab = -U_aa W,  W = sum_{c=a+1..b} M_ac U_cb   (by increasing b - a)
-     * so T_ba = U_ab^T = -W^T U_aa^T.  LDS (in the K / Q rows' space):
-     * MB the 10 upper blocks of M per value head, TB the 10 lower blocks of
-     * T, UD the diagonal blocks of U row-major; a block is 16 rows of BS
-     * floats (row stride 20 = 4 x odd: conflict-free 16-byte operand reads). */
-    float *MB = sbuf, *TB = sbuf + 2 * 10 * BLK, *UD = sbuf + 4 * 10 * BLK;
-
-    /* M blocks from the K K^T tiles: tile (tr >= tc) holds A[r][s] for r in
-     * block tr, s in block tc, i.e. M block (tc, tr), row s, columns r;
-     * Pm[r][s] = exp(G_r - G_s) q_r.k_s (s <= r) straight to its buffer */
-#pragma unroll
-    for (int k = 0; k < 5; k++) {
-        const int n = w + 4 * k, m = n % 10;
-        const int tr = m < 1 ? 0 : m < 3 ? 1 : m < 6 ? 2 : 3;
-        const int tc = m - (tr * (tr + 1)) / 2;
-        const int s = 16 * tc + l16;
-#pragma unroll
-        for (int v = 0; v < 2; v++) {
-            float o[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = 16 * tr + 4 * lq + i;
-                const float dec = __expf((float)(sG[v][r] - sG[v][s]));   /* v_exp_f32, ~1 ulp */
-                o[i] = n < 10 ? (s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f)
-                              : (s <= r ? dec * res[k][i] : 0.0f);
-            }
-            if (n < 10) {
-                *reinterpret_cast<float4 *>(&MB[(v * 10 + blk_q(tc, tr)) * BLK + l16 * BS + 4 * lq]) =
-                    make_float4(o[0], o[1], o[2], o[3]);
-            } else {
-                float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C + tri_idx(tr, tc) * 256;
-#pragma unroll
-                for (int i = 0; i < 4; i++) Pm[(4 * lq + i) * 16 + l16] = o[i];
+        /* the conv ring: slot pos % 4 <- raw row of pos for the last min(B, 4)
+         * tokens, written by the last chunk's items (the conv kernel, which
+         * reads the ring, has finished) */
+        if (c == p.n_chunks - 1) {
+            const int nr = min(p.B, 4), n4 = rows / 4;
+            for (int i = kh * 256 + t; i < nr * n4; i += KH * 256) {
+                const int b = p.B - nr + i / n4, c4 = 4 * (i % n4);
+                *reinterpret_cast<float4 *>(p.ring + (size_t)((p.t0 + b) & 3) * rows + c4) =
+                    *reinterpret_cast<const float4 *>(p.qkv + (size_t)b * rows + c4);
             }
         }
-    }
-    q35_lds_barrier();
 
-    /* diagonal blocks: wave w inverts block a = w of both value heads,
-     * column kc of U_aa on lane kc (+16 for head 1; lanes 32-63 repeat
-     * lanes 0-31 and do not write) */
-    {
-        const int a = w, v = (lane >> 4) & 1, kc = lane & 15;
-        const float *Md = MB + (v * 10 + blk_q(a, a)) * BLK;
-        float u[16];
-#pragma unroll
-        for (int s = 15; s >= 0; s--) {
-            float4 mrow[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) mrow[q] = *reinterpret_cast<const float4 *>(&Md[s * BS + 4 * q]);
-            float acc = s == kc ? 1.0f : 0.0f;
-#pragma unroll
-            for (int r = s + 1; r < 16; r++) acc = fmaf(-el(mrow[r >> 2], r & 3), u[r], acc);
-            u[s] = acc;
-        }
-        if (lane < 32) {
-            float *Td = TB + (v * 10 + blk_q(a, a)) * BLK + kc * BS;     /* T_aa row kc */
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                *reinterpret_cast<float4 *>(&Td[4 * q]) = make_float4(u[4 * q], u[4 * q + 1], u[4 * q + 2], u[4 * q + 3]);
-            float *Ud = UD + (v * 4 + a) * BLK;
-#pragma unroll
-            for (int s = 0; s < 16; s++) Ud[s * BS + kc] = u[s];
-        }
-    }
-    q35_lds_barrier();
-
-    /* off-diagonal blocks by distance d = b - a: jobs (head v, block a),
-     * dealt round-robin over the waves; each is two 16x16x16 products */
-#pragma unroll
-    for (int d = 1; d < 4; d++) {
-        for (int j = w; j < 2 * (4 - d); j += 4) {
-            const int v = j / (4 - d), a = j % (4 - d), b = a + d;
-            f32x4_t wacc = {0.f, 0.f, 0.f, 0.f};
-            for (int cb = a + 1; cb <= b; cb++) {
-                /* X = M_ac row-major; Y = U_cb, read as its transpose T_bc */
-                const float4 xa = *reinterpret_cast<const float4 *>(&MB[(v * 10 + blk_q(a, cb)) * BLK + l16 * BS + 4 * lq]);
-                const float4 yb = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(cb, b)) * BLK + l16 * BS + 4 * lq]);
-#pragma unroll
-                for (int e = 0; e < 4; e++) wacc = mfma4(el(xa, e), el(yb, e), wacc);
+        /* gates and the chunk-local cumulative log-decay of value head 2kh + w
+         * (pads: g = beta = 0) */
+        if (w < 2) {
+            const int h = 2 * kh + w;
+            float g = 0.f, beta = 0.f;
+            if (lane < nv) {
+                const float2 gb = *reinterpret_cast<const float2 *>(p.gates + ((size_t)(b0 + lane) * VH + h) * 2);
+                g = gb.x;
+                beta = gb.y;
             }
-            /* T_ba = (-W^T) U_aa^T: this lane's W entries W[4lq+e][l16] are
-             * X[l16][4lq+e] of -W^T as they stand; Y^T = U_aa row-major */
-            const float4 ud = *reinterpret_cast<const float4 *>(&UD[(v * 4 + a) * BLK + l16 * BS + 4 * lq]);
-            f32x4_t tb = {0.f, 0.f, 0.f, 0.f};
+            double G = g;
 #pragma unroll
-            for (int e = 0; e < 4; e++) tb = mfma4(-wacc[e], el(ud, e), tb);
-            float *Tt = TB + (v * 10 + blk_q(a, b)) * BLK;
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(G, off);
+                if (lane >= off) G += o;
+            }
+            sG[w][lane] = G;
+            sBeta[w][lane] = beta;
+            const double Gc = __shfl(G, 63);
+            float *gv = p.gvec + ((size_t)c * VH + h) * Q35_LIN_GVEC;
+            gv[lane] = (float)exp(G);
+            gv[C + lane] = (float)exp(Gc - G);
+            gv[2 * C + lane] = beta;
+            if (lane == 0) gv[3 * C] = (float)exp(Gc);
+        }
+        /* the item's K and Q rows into LDS (pad rows zero), then the next
+         * item's requested into the same registers */
 #pragma unroll
-            for (int i = 0; i < 4; i++) Tt[(4 * lq + i) * BS + l16] = tb[i];
+        for (int u = 0; u < 8; u++) {
+            const int idx = u * 256 + t, r = idx >> 5, c4 = (idx & 31) * 4;
+            *reinterpret_cast<float4 *>(&sK[sw128(r, c4)]) = R.k[u];
+            *reinterpret_cast<float4 *>(&sQ[sw128(r, c4)]) = R.q[u];
         }
         q35_lds_barrier();
-    }
+        if (it + (int)gridDim.x < n_items) chunk_rows_load(R, p, it + gridDim.x, rows);
 
-    /* T out: 2 heads x the 10 lower blocks x 16 rows x 4 float4, each wave
-     * instruction one whole 1 KB block */
+        /* K K^T and Q K^T, the 10 lower 16x16 tiles of each: tile n (0..19),
+         * wave w takes n = w, w+4, ..., w+16.  Lane l holds rows 4*(l/16)+i. */
+        f32x4_t res[5];
 #pragma unroll
-    for (int u = 0; u < 5; u++) {
-        const int idx = u * 256 + t, v = idx / 640, rem = idx % 640;
-        const int j = rem >> 6, r = (rem >> 2) & 15, q4 = rem & 3;
-        const int bb = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, ba = j - tri_idx(bb, 0);
-        const float4 o = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(ba, bb)) * BLK + r * BS + 4 * q4]);
-        *reinterpret_cast<float4 *>(p.T + ((size_t)c * VH + 2 * kh + v) * C * C + j * 256 + r * 16 + 4 * q4) = o;
+        for (int k = 0; k < 5; k++) {
+            const int n = w + 4 * k, m = n % 10;
+            const int tr = m < 1 ? 0 : m < 3 ? 1 : m < 6 ? 2 : 3;
+            const int tc = m - (tr * (tr + 1)) / 2;
+            const float *X = n < 10 ? sK : sQ;
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int blk = 0; blk < KD / 16; blk++) {
+                const float4 xa = *reinterpret_cast<const float4 *>(&X[sw128(16 * tr + l16, 16 * blk + 4 * lq)]);
+                const float4 yb = *reinterpret_cast<const float4 *>(&sK[sw128(16 * tc + l16, 16 * blk + 4 * lq)]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc = mfma4(el(xa, e), el(yb, e), acc);
+            }
+            res[k] = acc;
+        }
+        q35_lds_barrier();                       /* K and Q no longer read */
+
+        /* T = (I + A)^-1 in 16x16 blocks.  With M = A^T (strictly upper,
+         * M[s][r] = A[r][s]) and U = (I + M)^-1 = T^T, for blocks a <= b:
+         *   U_aa = (I + M_aa)^-1                      (back substitution)
+         *   U_ab = -U_aa W,  W = sum_{c=a+1..b} M_ac U_cb   (by increasing b - a)
+         * so T_ba = U_ab^T = -W^T U_aa^T.  LDS (in the K / Q rows' space):
+         * MB the 10 upper blocks of M per value head, TB the 10 lower blocks of
+         * T, UD the diagonal blocks of U row-major; a block is 16 rows of BS
+         * floats (row stride 20 = 4 x odd: conflict-free 16-byte operand reads). */
+        float *MB = sbuf, *TB = sbuf + 2 * 10 * BLK, *UD = sbuf + 4 * 10 * BLK;
+
+        /* M blocks from the K K^T tiles: tile (tr >= tc) holds A[r][s] for r in
+         * block tr, s in block tc, i.e. M block (tc, tr), row s, columns r;
+         * Pm[r][s] = exp(G_r - G_s) q_r.k_s (s <= r) straight to its buffer */
+#pragma unroll
+        for (int k = 0; k < 5; k++) {
+            const int n = w + 4 * k, m = n % 10;
+            const int tr = m < 1 ? 0 : m < 3 ? 1 : m < 6 ? 2 : 3;
+            const int tc = m - (tr * (tr + 1)) / 2;
+            const int s = 16 * tc + l16;
+#pragma unroll
+            for (int v = 0; v < 2; v++) {
+                float o[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 16 * tr + 4 * lq + i;
+                    const float dec = __expf((float)(sG[v][r] - sG[v][s]));   /* v_exp_f32, ~1 ulp */
+                    o[i] = n < 10 ? (s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f)
+                                  : (s <= r ? dec * res[k][i] : 0.0f);
+                }
+                if (n < 10) {
+                    *reinterpret_cast<float4 *>(&MB[(v * 10 + blk_q(tc, tr)) * BLK + l16 * BS + 4 * lq]) =
+                        make_float4(o[0], o[1], o[2], o[3]);
+                } else {
+                    float *Pm = p.Pm + ((size_t)c * VH + 2 * kh + v) * C * C + tri_idx(tr, tc) * 256;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) Pm[(4 * lq + i) * 16 + l16] = o[i];
+                }
+            }
+        }
+        q35_lds_barrier();
+
+        /* diagonal blocks: wave w inverts block a = w of both value heads,
+         * column kc of U_aa on lane kc (+16 for head 1; lanes 32-63 repeat
+         * lanes 0-31 and do not write) */
+        {
+            const int a = w, v = (lane >> 4) & 1, kc = lane & 15;
+            const float *Md = MB + (v * 10 + blk_q(a, a)) * BLK;
+            float u[16];
+#pragma unroll
+            for (int s = 15; s >= 0; s--) {
+                float4 mrow[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) mrow[q] = *reinterpret_cast<const float4 *>(&Md[s * BS + 4 * q]);
+                float acc = s == kc ? 1.0f : 0.0f;
+#pragma unroll
+                for (int r = s + 1; r < 16; r++) acc = fmaf(-el(mrow[r >> 2], r & 3), u[r], acc);
+                u[s] = acc;
+            }
+            if (lane < 32) {
+                float *Td = TB + (v * 10 + blk_q(a, a)) * BLK + kc * BS;     /* T_aa row kc */
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    *reinterpret_cast<float4 *>(&Td[4 * q]) = make_float4(u[4 * q], u[4 * q + 1], u[4 * q + 2], u[4 * q + 3]);
+                float *Ud = UD + (v * 4 + a) * BLK;
+#pragma unroll
+                for (int s = 0; s < 16; s++) Ud[s * BS + kc] = u[s];
+            }
+        }
+        q35_lds_barrier();
+
+        /* off-diagonal blocks by distance d = b - a: jobs (head v, block a),
+         * dealt round-robin over the waves; each is two 16x16x16 products */
+#pragma unroll
+        for (int d = 1; d < 4; d++) {
+            for (int j = w; j < 2 * (4 - d); j += 4) {
+                const int v = j / (4 - d), a = j % (4 - d), b = a + d;
+                f32x4_t wacc = {0.f, 0.f, 0.f, 0.f};
+                for (int cb = a + 1; cb <= b; cb++) {
+                    /* X = M_ac row-major; Y = U_cb, read as its transpose T_bc */
+                    const float4 xa = *reinterpret_cast<const float4 *>(&MB[(v * 10 + blk_q(a, cb)) * BLK + l16 * BS + 4 * lq]);
+                    const float4 yb = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(cb, b)) * BLK + l16 * BS + 4 * lq]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) wacc = mfma4(el(xa, e), el(yb, e), wacc);
+                }
+                /* T_ba = (-W^T) U_aa^T: this lane's W entries W[4lq+e][l16] are
+                 * X[l16][4lq+e] of -W^T as they stand; Y^T = U_aa row-major */
+                const float4 ud = *reinterpret_cast<const float4 *>(&UD[(v * 4 + a) * BLK + l16 * BS + 4 * lq]);
+                f32x4_t tb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; e++) tb = mfma4(-wacc[e], el(ud, e), tb);
+                float *Tt = TB + (v * 10 + blk_q(a, b)) * BLK;
+#pragma unroll
+                for (int i = 0; i < 4; i++) Tt[(4 * lq + i) * BS + l16] = tb[i];
+            }
+            q35_lds_barrier();
+        }
+
+        /* T out: 2 heads x the 10 lower blocks x 16 rows x 4 float4, each wave
+         * instruction one whole 1 KB block */
+#pragma unroll
+        for (int u = 0; u < 5; u++) {
+            const int idx = u * 256 + t, v = idx / 640, rem = idx % 640;
+            const int j = rem >> 6, r = (rem >> 2) & 15, q4 = rem & 3;
+            const int bb = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, ba = j - tri_idx(bb, 0);
+            const float4 o = *reinterpret_cast<const float4 *>(&TB[(v * 10 + blk_q(ba, bb)) * BLK + r * BS + 4 * q4]);
+            *reinterpret_cast<float4 *>(p.T + ((size_t)c * VH + 2 * kh + v) * C * C + j * 256 + r * 16 + 4 * q4) = o;
+        }
+        q35_lds_barrier();                       /* T read out: the next item may overwrite the LDS */
     }
 }
 
@@ -801,7 +837,7 @@ extern "C" hipError_t q35_lin_prefill(const Q35LinPrefill *pin, hipStream_t stre
     hipLaunchKernelGGL(conv_kernel, dim3(rows / 1024, (p.B + CT - 1) / CT), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(chunk_kernel, dim3(p.n_chunks, p.k_heads), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(chunk_kernel, dim3(min(p.n_chunks * p.k_heads, CHUNK_GRID)), dim3(256), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(scan_kernel, dim3(p.v_heads * (VD / 16)), dim3(SCAN_THREADS), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
