@@ -77,20 +77,31 @@ __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
     /* k_heads is even, so both groups of a wave are q, both k or both v */
     const bool normed = grp < 2 * KH;
 
-    /* raw rows of positions t0+bb-3 .. t0+bb+CT-1 */
+    /* the conv weights first, then the raw rows of positions t0+bb-3 ..
+     * t0+bb+CT-1 in order, all unconditional range-checked buffer loads
+     * (rows past the batch and positions before 0, addressed at the ring
+     * view's end, read as zero): loads
+     * complete in issue order, so token j's outputs wait only for the rows
+     * up to j + 3 and its stores go out while the later rows arrive.  The
+     * row view starts at the block's first row at or after row 0, so its
+     * 32-bit offsets cover any batch length. */
+    const uint4 wa = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4);
+    const uint4 wb = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4 + 8);
+    const int r0 = max(bb - 3, 0);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<float *>(p.qkv) + (size_t)r0 * rows), 0,
+        min(p.B - r0, CT + 3) * rows * 4, Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(p.ring), 0, 4 * rows * 4, Q35_BUF_DW3);
     float4 xr[CT + 3];
 #pragma unroll
     for (int k = 0; k < CT + 3; k++) {
-        const int b = bb - 3 + k, pp = p.t0 + b;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (b >= 0 && b < p.B)
-            v = *reinterpret_cast<const float4 *>(p.qkv + (size_t)b * rows + c0);
-        else if (b < 0 && pp >= 0)
-            v = *reinterpret_cast<const float4 *>(p.ring + (size_t)(pp & 3) * rows + c0);
-        xr[k] = v;
+        const int b = bb - 3 + k, pp = p.t0 + b;     /* block-uniform */
+        const __amdgpu_buffer_rsrc_t rs = b >= 0 ? rq : rr;
+        const uint32_t off = b >= 0 ? (uint32_t)(((b - r0) * rows + c0) * 4)
+                             : pp >= 0 ? (uint32_t)(((pp & 3) * rows + c0) * 4) : (uint32_t)(4 * rows * 4);
+        xr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
-    const uint4 wa = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4);
-    const uint4 wb = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)c0 * 4 + 8);
     const uint2 wt[4] = {make_uint2(wa.x, wa.y), make_uint2(wa.z, wa.w), make_uint2(wb.x, wb.y),
                          make_uint2(wb.z, wb.w)};
     const float scale = grp < KH ? 1.0f / (float)KD : 1.0f / sqrtf((float)KD);
