@@ -142,21 +142,34 @@ __device__ __forceinline__ void vprep_block(const Q35GqaPrefill &p, int bx, int 
     const int kb = (p.t0 >> 5) + bx;
     const int t = threadIdx.x;
     __shared__ float sv[32][D + 1];
-    /* rows: key r of the block is position 32kb + r */
+    /* rows: key r of the block is position 32kb + r.  All eight loads of a
+     * thread go out before any is used, as range-checked buffer loads
+     * (positions before t0 addressed at the view's end, rows past the batch
+     * beyond it: both read zero); as guarded loads each waited for the one
+     * before it, eight memory round trips in a row. */
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<float *>(p.v_in)), 0, p.B * p.kv_heads * D * 4, Q35_BUF_DW3);
+    float4 vv[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
         const int idx = u * 256 + t, r = idx >> 6, c4 = (idx & 63) * 4;
-        const int pos = 32 * kb + r;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (pos >= p.t0 && pos < p.t0 + p.B)
-            v = *reinterpret_cast<const float4 *>(p.v_in + ((size_t)(pos - p.t0) * p.kv_heads + g) * D + c4);
-        q35_f16_guard(p.status, Q35_STATUS_GQA_F16, q35_f16_over(v.x) || q35_f16_over(v.y) ||
-                                                        q35_f16_over(v.z) || q35_f16_over(v.w));
+        const int b = 32 * kb + r - p.t0;
+        const uint32_t off = b >= 0 ? (uint32_t)(((b * p.kv_heads + g) * D + c4) * 4)
+                                    : (uint32_t)(p.B * p.kv_heads * D * 4);
+        vv[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+    }
+    bool over = false;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int idx = u * 256 + t, r = idx >> 6, c4 = (idx & 63) * 4;
+        const float4 v = vv[u];
+        over = over || q35_f16_over(v.x) || q35_f16_over(v.y) || q35_f16_over(v.z) || q35_f16_over(v.w);
         sv[r][c4] = v.x;
         sv[r][c4 + 1] = v.y;
         sv[r][c4 + 2] = v.z;
         sv[r][c4 + 3] = v.w;
     }
+    q35_f16_guard(p.status, Q35_STATUS_GQA_F16, over);
     q35_lds_barrier();
     const bool whole = 32 * kb >= p.t0 && 32 * kb + 32 <= p.t0 + p.B;   /* block-uniform */
     /* workspace: lane (d, granule q of 4 a dim row), slots 8q..8q+7 */
