@@ -82,21 +82,38 @@ __device__ __forceinline__ int wslot(int r, int h) { return h ^ (((r >> 2) ^ (r 
  * square sum times the hardware rsq (about 1 ulp from the reference's double
  * sum and division, src/attn_qwen.c:142-157, far below the hi / lo split's
  * 22 bits). */
+constexpr int XW = 8192 / (8 * NT);     /* words a thread holds (K <= 8192) */
 __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const int nw = p.K / 8;
     const bool live = m < p.M;
-    const float *x = p.x + (size_t)m * p.ldx;
     __shared__ float sred[NT / 64];
+
+    /* the thread's words of the row and of the norm weight, all requested
+     * at once as range-checked buffer loads (rows past M, words past K and
+     * an absent norm weight read as zeros): the norm and the conversion
+     * then work from registers, one memory round trip a workgroup */
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<float *>(live ? p.x + (size_t)m * p.ldx : p.x)), 0, live ? p.K * 4 : 0,
+        Q35_BUF_DW3);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        q35_uniform_ptr(const_cast<uint16_t *>(p.norm_w)), 0, p.norm_w ? p.K * 2 : 0, Q35_BUF_DW3);
+    float4 xa[XW], xb[XW];
+    uint4 wv[XW];
+#pragma unroll
+    for (int i = 0; i < XW; i++) {
+        const int v = t + i * NT;
+        xa[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xrs, 32 * v, 0, 0));
+        xb[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xrs, 32 * v + 16, 0, 0));
+        wv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs, 16 * v, 0, 0));
+    }
 
     float ri = 1.0f;
     if (p.norm_w) {
         float ss = 0.0f;
-        for (int v = t; v < nw; v += NT) {
-            if (!live) break;
-            const float4 a = *reinterpret_cast<const float4 *>(x + 8 * v);
-            const float4 b = *reinterpret_cast<const float4 *>(x + 8 * v + 4);
-            const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < XW; i++) {
+            const float e[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
 #pragma unroll
             for (int j = 0; j < 8; j++) ss = fmaf(e[j], e[j], ss);
         }
@@ -106,20 +123,16 @@ __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
         ss = (sred[0] + sred[1]) + (sred[2] + sred[3]);
         ri = __builtin_amdgcn_rsqf(ss * (1.0f / (float)p.K) + 1e-6f);
     }
-    for (int v = t; v < nw; v += NT) {
-        float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (live) {
-            const float4 a = *reinterpret_cast<const float4 *>(x + 8 * v);
-            const float4 b = *reinterpret_cast<const float4 *>(x + 8 * v + 4);
-            e[0] = a.x, e[1] = a.y, e[2] = a.z, e[3] = a.w;
-            e[4] = b.x, e[5] = b.y, e[6] = b.z, e[7] = b.w;
-            if (p.norm_w) {
-                const uint4 wb = *reinterpret_cast<const uint4 *>(p.norm_w + 8 * v);
-                const uint32_t ww[4] = {wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    e[j] = e[j] * ri * q35_bf2f((uint16_t)(ww[j >> 1] >> (16 * (j & 1))));
-            }
+    for (int i = 0; i < XW; i++) {
+        const int v = t + i * NT;
+        if (v >= nw) break;   /* nw is a multiple of 8: the 8 lanes of a group (q35_sum8) leave together */
+        float e[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+        if (p.norm_w) {
+            const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                e[j] = e[j] * ri * q35_bf2f((uint16_t)(ww[j >> 1] >> (16 * (j & 1))));
         }
         bool over = false;
 #pragma unroll
