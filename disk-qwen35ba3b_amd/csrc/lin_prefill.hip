@@ -56,17 +56,21 @@ __device__ __forceinline__ float el(const float4 &v, int e) {
 }
 
 /* ---- 1. conv + SiLU, q/k norms, gates ------------------------------------ *
- * grid (rows / 1024, ceil(B / 16)), 4 waves; wave w owns channels
+ * grid (rows / 1024, ceil(B / CT)), 4 waves; wave w owns channels
  * 256 (4 blockIdx.x + w) .. +255, two 128-channel head groups (q heads,
  * then k heads, then v heads), one per half-wave, 4 channels a lane, for
- * 16 consecutive tokens: the 19 raw rows they tap are loaded once (a
- * sliding window instead of 4 loads per output).  The q / k norm of a
+ * CT = 6 consecutive tokens: the 9 raw rows they tap are loaded once (a
+ * sliding window instead of 4 loads per output).  Of CT = 4, 6, 8, 12, 16,
+ * 24, 32 tokens a workgroup, 6 is the fastest (rocprof at 4096 tokens:
+ * 47.9, 46.6, 48.4, 51.6, 53.2, 55.8, 58.2 us): the window's re-read rows
+ * are served by the cache, and more, smaller workgroups keep more waves
+ * streaming.  The q / k norm of a
  * head is a half-wave sum.  Against the reference's per-element IEEE
  * divisions and double square sums, the SiLU uses v_exp_f32 / v_rcp_f32,
  * the norm one reciprocal per token (each about 1 ulp) and an fp32 square
  * sum (128 terms, at most 8e-6 relative, about 1e-7 in practice): the
  * kernel then runs at the HBM rate of its 2 x B x rows x 4 bytes. */
-constexpr int CT = 16;
+constexpr int CT = 6;
 __global__ __launch_bounds__(256) void conv_kernel(Q35LinPrefill p) {
     const int bb = blockIdx.y * CT;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
