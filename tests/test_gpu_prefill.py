@@ -183,11 +183,13 @@ def _lin_check(ga, cache, ring, S0, w, t0, qkv, z, a, b, what):
 
 
 @pytest.mark.parametrize("T,t0", [(1, 0), (3, 0), (5, 0), (64, 0), (65, 0), (200, 0),
-                                  (1, 9), (2, 9), (130, 7)])
+                                  (1, 9), (2, 9), (130, 7), (2100, 5)])
 def test_lin_prefill_chunked_vs_serial(T, t0):
     """Chunk boundaries (64), ragged last chunks, B < 4 (ring keeps older
     rows), a prefill continuing at an unaligned position with a past state
-    and conv history."""
+    and conv history; at 2100 tokens the chunk kernel's 528 (chunk, key
+    head) items exceed its 512 workgroups, so 16 of them take a second,
+    ragged item."""
     ga, cache, ring, S0, w = _lin_binding(t0 + T + 8, t0, 11, zero_state=(t0 == 0))
     qkv, z, a, b = W.lin_tokens(LG, T, 11)
     _lin_check(ga, cache, ring, S0, w, t0, qkv, z, a, b, f"lin prefill T={T} t0={t0}")
