@@ -196,6 +196,7 @@ __device__ __forceinline__ void chunk_rows_load(ChunkRows &R, const Q35LinPrefil
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_kernel(Q35LinPrefill p) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __builtin_assume(w >= 0 && w < 4);     /* 256 threads: tile n = w + 4k is K K^T for k < 2, Q K^T for k > 2 */
     const int KH = p.k_heads, VH = p.v_heads;
     const int rows = 2 * KH * KD + VH * VD;
     const int n_items = p.n_chunks * KH;
@@ -203,8 +204,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     /* K and Q rows, later A^T of both value heads, later T of both */
     __shared__ __align__(16) float sbuf[2 * C * KD];
     float *sK = sbuf, *sQ = sbuf + C * KD;
-    __shared__ double sG[2][C];
-    __shared__ float sBeta[2][C];
+    __shared__ __align__(16) double sG[2][C];
+    __shared__ __align__(16) float sBeta[2][C];
 
     ChunkRows R;
     chunk_rows_load(R, p, blockIdx.x, rows);
@@ -306,15 +307,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int tr = m < 1 ? 0 : m < 3 ? 1 : m < 6 ? 2 : 3;
             const int tc = m - (tr * (tr + 1)) / 2;
             const int s = 16 * tc + l16;
+            const int r0 = 16 * tr + 4 * lq;
 #pragma unroll
             for (int v = 0; v < 2; v++) {
+                /* the lane's G_s, its four G_r and beta_r read up front, the
+                 * masks as selects: no LDS read waits inside a branch */
+                const double gs = sG[v][s];
+                const double2 g01 = *reinterpret_cast<const double2 *>(&sG[v][r0]);
+                const double2 g23 = *reinterpret_cast<const double2 *>(&sG[v][r0 + 2]);
+                const float4 bt = *reinterpret_cast<const float4 *>(&sBeta[v][r0]);
+                const double gr[4] = {g01.x, g01.y, g23.x, g23.y};
+                const float br[4] = {bt.x, bt.y, bt.z, bt.w};
                 float o[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int r = 16 * tr + 4 * lq + i;
-                    const float dec = __expf((float)(sG[v][r] - sG[v][s]));   /* v_exp_f32, ~1 ulp */
-                    o[i] = n < 10 ? (s < r ? sBeta[v][r] * dec * res[k][i] : 0.0f)
-                                  : (s <= r ? dec * res[k][i] : 0.0f);
+                    const int r = r0 + i;
+                    const float dec = __expf((float)(gr[i] - gs));   /* v_exp_f32, ~1 ulp */
+                    const float av = br[i] * dec * res[k][i], pv = dec * res[k][i];
+                    o[i] = n < 10 ? (s < r ? av : 0.0f) : (s <= r ? pv : 0.0f);
                 }
                 if (n < 10) {
                     *reinterpret_cast<float4 *>(&MB[(v * 10 + blk_q(tc, tr)) * BLK + l16 * BS + 4 * lq]) =
