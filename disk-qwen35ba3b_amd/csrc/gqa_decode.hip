@@ -160,6 +160,8 @@ __device__ __forceinline__ void attend_tile(KTile &kt, VTile &vt, const bf16x8_t
 }
 
 __global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
+    q35_args_now(p.q_gate, p.k_new, p.v_new, p.qn_w, p.kn_w, p.rope, p.kt, p.vt, p.part_o, p.part_ml,
+                 p.attn_out, p.k_post, p.token, p.t_tiles, p.heads, p.kv_heads, p.chunk, p.n_chunks);
     const int c = blockIdx.x, g = blockIdx.y;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int n_past = p.token;

@@ -43,6 +43,8 @@ namespace {
 constexpr int KD = 128, VD = 128, NT = 1024;
 
 __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
+    q35_args_now(p.qkv, p.z, p.a, p.b, p.conv_w, p.dt_bias, p.norm_w, p.A_log, p.ring, p.state, p.out,
+                 p.qkv_post, p.token, p.k_heads, p.v_heads);
     const int h = blockIdx.x;      /* value head */
     const int kh = h >> 1;         /* its key head (src/attn_qwen.c:658) */
     const int t = threadIdx.x;
