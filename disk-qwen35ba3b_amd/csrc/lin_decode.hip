@@ -42,13 +42,24 @@ namespace {
 
 constexpr int KD = 128, VD = 128, NT = 1024;
 
-__global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
-    q35_args_now(p.qkv, p.z, p.a, p.b, p.conv_w, p.dt_bias, p.norm_w, p.A_log, p.ring, p.state, p.out,
-                 p.qkv_post, p.token, p.k_heads, p.v_heads);
+/* The arguments are scalars, not the struct, so that the first nine (14
+ * dwords: everything the conv inputs and the state loads need) are
+ * preloaded into SGPRs at wave launch (-amdgpu-kernarg-preload-count=9 for
+ * this file): the kernel's first global loads wait for no argument load. */
+__global__ __launch_bounds__(NT) void lin_decode_kernel(int token, int rows, int k_heads, int v_heads,
+                                                        const float *qkv, float *ring,
+                                                        const uint16_t *conv_w, float *state,
+                                                        const float *a, const float *b,
+                                                        const float *A_log, const uint16_t *dt_bias,
+                                                        const float *z, const uint16_t *norm_w, float *out,
+                                                        float *qkv_post) {
+    Q35LinDecode p;
+    p.token = token, p.k_heads = k_heads, p.v_heads = v_heads;
+    p.qkv = qkv, p.ring = ring, p.conv_w = conv_w, p.state = state, p.a = a, p.b = b;
+    p.A_log = A_log, p.dt_bias = dt_bias, p.z = z, p.norm_w = norm_w, p.out = out, p.qkv_post = qkv_post;
     const int h = blockIdx.x;      /* value head */
     const int kh = h >> 1;         /* its key head (src/attn_qwen.c:658) */
     const int t = threadIdx.x;
-    const int rows = 2 * p.k_heads * KD + p.v_heads * VD;
     const int tok = p.token;
 
     /* ---- every global input in flight at once ---- */
@@ -79,6 +90,8 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
         xin[3] = *reinterpret_cast<const float2 *>(p.qkv + ch);
         wv = *reinterpret_cast<const uint4 *>(p.conv_w + (size_t)ch * 4);
     }
+#pragma unroll
+    for (int u = 0; u < 4; u++) s[u] = sp[64 * u];
     /* the gated norm's inputs: wave 3 owns the head's 128 outputs, 2 a lane */
     float2 zv = make_float2(0.f, 0.f);
     uint32_t nw = 0;
@@ -96,9 +109,6 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
     const float ga = p.a[h], gb = p.b[h], gal = p.A_log[h];
     const int dt_hi = (int)((reinterpret_cast<uintptr_t>(p.dt_bias + h) >> 1) & 1);
     const uint16_t gdt = (uint16_t)(*reinterpret_cast<const uint32_t *>(p.dt_bias + h - dt_hi) >> (16 * dt_hi));
-
-#pragma unroll
-    for (int u = 0; u < 4; u++) s[u] = sp[64 * u];
     __shared__ float sq[KD], sk[KD], sv[VD], so[VD];
     __shared__ float sgate[2];
 
@@ -203,6 +213,9 @@ __global__ __launch_bounds__(NT) void lin_decode_kernel(Q35LinDecode p) {
 }  // namespace
 
 extern "C" hipError_t q35_lin_decode(const Q35LinDecode *p, hipStream_t stream) {
-    hipLaunchKernelGGL(lin_decode_kernel, dim3(p->v_heads), dim3(NT), 0, stream, *p);
+    hipLaunchKernelGGL(lin_decode_kernel, dim3(p->v_heads), dim3(NT), 0, stream, p->token,
+                       2 * p->k_heads * KD + p->v_heads * VD, p->k_heads, p->v_heads, p->qkv, p->ring,
+                       p->conv_w, p->state, p->a, p->b, p->A_log, p->dt_bias, p->z, p->norm_w, p->out,
+                       p->qkv_post);
     return hipGetLastError();
 }
