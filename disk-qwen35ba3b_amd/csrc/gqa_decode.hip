@@ -159,9 +159,21 @@ __device__ __forceinline__ void attend_tile(KTile &kt, VTile &vt, const bf16x8_t
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt.v[dt], pb, acc[dt], 0, 0, 0);
 }
 
-__global__ __launch_bounds__(NT) void gqa_split_kernel(Q35GqaDecode p) {
-    q35_args_now(p.q_gate, p.k_new, p.v_new, p.qn_w, p.kn_w, p.rope, p.kt, p.vt, p.part_o, p.part_ml,
-                 p.attn_out, p.k_post, p.token, p.t_tiles, p.heads, p.kv_heads, p.chunk, p.n_chunks);
+/* The arguments are scalars, not the struct, so that the first nine (14
+ * dwords: what the prologue and the first K/V tiles need) are preloaded
+ * into SGPRs at wave launch (-amdgpu-kernarg-preload-count=9 for this
+ * file); the rest load while those loads are in flight. */
+__global__ __launch_bounds__(NT) void gqa_split_kernel(int token, int t_tiles, int chunk, int n_chunks,
+                                                       const float *q_gate, const uint16_t *qn_w,
+                                                       const float *rope, uint16_t *kt, uint16_t *vt,
+                                                       const float *k_new, const float *v_new,
+                                                       const uint16_t *kn_w, float *part_o, float *part_ml,
+                                                       float *k_post, int heads, int kv_heads) {
+    Q35GqaDecode p;
+    p.token = token, p.t_tiles = t_tiles, p.chunk = chunk, p.n_chunks = n_chunks;
+    p.q_gate = q_gate, p.qn_w = qn_w, p.rope = rope, p.kt = kt, p.vt = vt;
+    p.k_new = k_new, p.v_new = v_new, p.kn_w = kn_w, p.part_o = part_o, p.part_ml = part_ml;
+    p.k_post = k_post, p.heads = heads, p.kv_heads = kv_heads, p.attn_out = nullptr;
     const int c = blockIdx.x, g = blockIdx.y;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int n_past = p.token;
@@ -377,7 +389,12 @@ __device__ __forceinline__ float wave_max(float v) {
     return pair_max32(pair_max16(v));
 }
 template <int MCH>
-__global__ __launch_bounds__(64) void gqa_merge_kernel(Q35GqaDecode p) {
+__global__ __launch_bounds__(64) void gqa_merge_kernel(int n_chunks, int heads, const float *part_ml,
+                                                       const float *part_o, const float *q_gate,
+                                                       float *attn_out) {
+    Q35GqaDecode p;
+    p.n_chunks = n_chunks, p.heads = heads, p.part_ml = const_cast<float *>(part_ml);
+    p.part_o = const_cast<float *>(part_o), p.q_gate = q_gate, p.attn_out = attn_out;
     const int h = blockIdx.x, g = h / G, hh = h % G, d0 = 16 * blockIdx.y;
     const int lane = threadIdx.x;
     const int P = p.n_chunks;
@@ -474,13 +491,16 @@ extern "C" int q35_gqa_max_chunks(void) { return MAX_CHUNKS; }
 extern "C" hipError_t q35_gqa_decode(const Q35GqaDecode *p, hipStream_t stream) {
     if (p->heads != p->kv_heads * G || p->n_chunks < 1 || p->n_chunks > MAX_CHUNKS)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gqa_split_kernel, dim3(p->n_chunks, p->kv_heads),
-                       dim3(NT), 0, stream, *p);
+    hipLaunchKernelGGL(gqa_split_kernel, dim3(p->n_chunks, p->kv_heads), dim3(NT), 0, stream, p->token,
+                       p->t_tiles, p->chunk, p->n_chunks, p->q_gate, p->qn_w, p->rope, p->kt, p->vt, p->k_new,
+                       p->v_new, p->kn_w, p->part_o, p->part_ml, p->k_post, p->heads, p->kv_heads);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p->n_chunks <= 128)
-        hipLaunchKernelGGL(gqa_merge_kernel<2>, dim3(p->heads, D / 16), dim3(64), 0, stream, *p);
+        hipLaunchKernelGGL(gqa_merge_kernel<2>, dim3(p->heads, D / 16), dim3(64), 0, stream, p->n_chunks,
+                           p->heads, p->part_ml, p->part_o, p->q_gate, p->attn_out);
     else
-        hipLaunchKernelGGL(gqa_merge_kernel<MAX_CHUNKS / 64>, dim3(p->heads, D / 16), dim3(64), 0, stream, *p);
+        hipLaunchKernelGGL(gqa_merge_kernel<MAX_CHUNKS / 64>, dim3(p->heads, D / 16), dim3(64), 0, stream,
+                           p->n_chunks, p->heads, p->part_ml, p->part_o, p->q_gate, p->attn_out);
     return hipGetLastError();
 }
