@@ -80,8 +80,19 @@ __device__ __forceinline__ float nib_dot(u32x4_t w, const float (&x)[32]) {
 template <int NCH>
 constexpr int rows_per_wave() { return NCH >= 4 ? 1 : 4 / NCH; }
 
+/* The arguments are scalars, not the struct, so that the first nine (14
+ * dwords: the row count, width, accumulate flag and the x, job table,
+ * norm weight, word and scale pointers) are preloaded into SGPRs at launch
+ * (-amdgpu-kernarg-preload-count=9 for this file): the job table and x go
+ * out with no argument load before them. */
 template <int NCH, bool NORM>
-__global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
+__global__ __launch_bounds__(NT) void mlx4_kernel(int R_, int C_, int accumulate, const float *x,
+                                                  const Q35Mlx4Job *jobs, const uint16_t *x_norm,
+                                                  const uint32_t *vals, const uint16_t *scales,
+                                                  const uint16_t *biases, float *y) {
+    Q35Mlx4 p;
+    p.R = R_, p.C = C_, p.accumulate = accumulate, p.x = x, p.y = y, p.jobs = jobs;
+    p.x_norm = x_norm, p.vals = vals, p.scales = scales, p.biases = biases;
     constexpr int RP = rows_per_wave<NCH>();
     Mlx4Job j;
     if (p.jobs) {
@@ -265,9 +276,11 @@ __global__ __launch_bounds__(NT) void mlx4_kernel(Q35Mlx4 p) {
 template <int NCH>
 void launch(const Q35Mlx4 *p, dim3 grid, hipStream_t stream) {
     if (p->x_norm)
-        hipLaunchKernelGGL((mlx4_kernel<NCH, true>), grid, dim3(NT), 0, stream, *p);
+        hipLaunchKernelGGL((mlx4_kernel<NCH, true>), grid, dim3(NT), 0, stream, p->R, p->C, p->accumulate,
+                           p->x, p->jobs, p->x_norm, p->vals, p->scales, p->biases, p->y);
     else
-        hipLaunchKernelGGL((mlx4_kernel<NCH, false>), grid, dim3(NT), 0, stream, *p);
+        hipLaunchKernelGGL((mlx4_kernel<NCH, false>), grid, dim3(NT), 0, stream, p->R, p->C, p->accumulate,
+                           p->x, p->jobs, p->x_norm, p->vals, p->scales, p->biases, p->y);
 }
 
 }  // namespace
