@@ -26,23 +26,6 @@ __device__ __forceinline__ T *q35_uniform_ptr(T *ptr) {
     return (T *)(((uint64_t)hi << 32) | lo);
 }
 
-/* Kernel arguments into SGPRs at a kernel's entry.  Left to itself the
- * compiler issues each group of scalar argument loads where its values are
- * first used, often inside a branch that an earlier group decides, so a
- * decode kernel paid two or three argument round trips one after another
- * before its first global load.  An empty asm that reads every argument
- * makes them all load at once, one round trip.  The asm only reads them,
- * so the pointers keep their global address space (a pointer passed out
- * of an asm would turn its loads into flat ones). */
-template <typename T>
-__device__ __forceinline__ void q35_arg_now(const T &v) {
-    asm volatile("" ::"s"(v));
-}
-template <typename... T>
-__device__ __forceinline__ void q35_args_now(const T &...v) {
-    (q35_arg_now(v), ...);
-}
-
 /* dword 3 of a raw buffer resource on gfx9-family GPUs (no format
  * conversion, range checking against num_records: loads outside the range
  * return zero, stores outside it are dropped) */
