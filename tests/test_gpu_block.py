@@ -5,12 +5,14 @@ linear_step :837-968).  input_layernorm, the MLX 4-bit projections, the
 core, the output projection and the residual all run on the device.
 
 Tolerance: the path's bar of 2e-3 on outputs, applied to the hidden state
-after every layer element by element relative to its magnitude above 1:
-|gpu - oracle| <= 2e-3 * max(1, |oracle|).  The state is fp32 of magnitude up
-to about 5 (a residual stream, not a bf16-stored attention output); the
-device keeps the KV cache in bf16 and the prefill attention's operands in
-fp16, whose roundings reach the state through the output projection.  The
-relative RMS is printed beside every check.
+after every layer as a maximum absolute error: |gpu - oracle| <= 2e-3
+elementwise.  The state is fp32 of magnitude up to about 9 (a residual
+stream, not a bf16-stored attention output); the device keeps the KV cache
+in bf16 and the prefill attention's operands in fp16, whose roundings reach
+the state through the output projection.  The largest error of these tests
+is 1.96e-3, a GQA layer step at position 40 whose state reaches 9.1 (the
+same check relative to max(1, |oracle|) gives 1.76e-3).  The relative RMS
+is printed beside every check.
 """
 import sys
 
@@ -37,9 +39,9 @@ def _say(msg):
 
 
 def _err(got, ref):
-    """(max |d| / max(1, |ref|) elementwise, relative RMS)"""
+    """(max |d| elementwise, relative RMS)"""
     got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    mx = float((np.abs(got - ref) / np.maximum(1.0, np.abs(ref))).max())
+    mx = float(np.abs(got - ref).max())
     rr = float(np.sqrt(((got - ref) ** 2).sum() / max((ref ** 2).sum(), 1e-300)))
     return mx, rr
 
@@ -91,7 +93,7 @@ def test_single_layer_steps(kind):
             st_g = ga.attn_step(0, tok, st_g)
             st_o = _oracle_layer(kind, ref[0], ws[0], tok, st_o)
             mx, rr = _err(st_g, st_o)
-            _say(f"  max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"  max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
     finally:
         ga.close()
@@ -111,7 +113,7 @@ def test_four_layer_stack_three_tokens():
                 st_g = ga.attn_step(L, tok, st_g)
                 st_o = _oracle_layer(k, ref[L], ws[L], tok, st_o)
             mx, rr = _err(st_g, st_o)
-            _say(f"stack token {tok}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"stack token {tok}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
         # the device state agrees with the oracle's after the steps; the
         # ring holds raw projection rows, equal up to the matvecs' fp32
@@ -175,7 +177,7 @@ def test_step_graph_replays_match_oracle():
             for Lr, k in enumerate(kinds):
                 st_o = _oracle_layer(k, ref[Lr], ws[Lr], n_past + s, st_o)
             mx, rr = _err(got, st_o)
-            _say(f"graph replay token {n_past + s}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"graph replay token {n_past + s}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
     finally:
         ga.close()
@@ -198,7 +200,7 @@ def test_chunk_matches_oracle(kind, t0, B):
             ring, S = ref[0]
             exp = O.lin_chunk(ring, S, t0, states, ws[0], LG.k_heads, LG.v_heads, LG.kd, LG.vd)
         mx, rr = _err(got, exp)
-        _say(f"  chunk max scaled err {mx:.3e} rel-rms {rr:.3e}")
+        _say(f"  chunk max abs err {mx:.3e} rel-rms {rr:.3e}")
         assert mx <= ATOL
         if kind == 2:
             # the device cache holds the chunk's k / v rows in bf16: the
@@ -210,7 +212,7 @@ def test_chunk_matches_oracle(kind, t0, B):
             st_g = ga.attn_step(0, tok, st_g)
             st_o = _oracle_layer(kind, ref[0], ws[0], tok, st_o)
             mx, rr = _err(st_g, st_o)
-            _say(f"  decode after chunk, token {tok}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"  decode after chunk, token {tok}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
     finally:
         ga.close()
@@ -257,10 +259,10 @@ def test_gqa_chunk_4096_sampled():
         with ThreadPoolExecutor(max_workers=12) as pool:   # the oracle releases the GIL
             for t, e in pool.map(check, samples):
                 if t % 512 == 511 or t < 100:
-                    _say(f"  token {t}: max scaled err {e[0]:.3e} rel-rms {e[1]:.3e}")
+                    _say(f"  token {t}: max abs err {e[0]:.3e} rel-rms {e[1]:.3e}")
                 if e[0] > worst:
                     worst, worst_t = e[0], t
-        _say(f"  sampled tokens {len(samples)}: worst max scaled err {worst:.3e} (token {worst_t})")
+        _say(f"  sampled tokens {len(samples)}: worst max abs err {worst:.3e} (token {worst_t})")
         assert worst <= ATOL
     finally:
         ga.close()
@@ -285,7 +287,7 @@ def test_chunk_past_the_cache_end(kind):
             exp = O.lin_chunk(ring, S, t0, states, ws[0], LG.k_heads, LG.v_heads, LG.kd, LG.vd,
                               max_tokens=mt)
         mx, rr = _err(got, exp)
-        _say(f"chunk kind {kind} t0 {t0} B 5 max_tokens {mt}: max scaled err {mx:.3e}")
+        _say(f"chunk kind {kind} t0 {t0} B 5 max_tokens {mt}: max abs err {mx:.3e}")
         assert mx <= ATOL
         assert np.array_equal(got[3:], states[3:]) and np.array_equal(exp[3:], states[3:])
         assert not np.array_equal(got[:3], states[:3])
@@ -313,7 +315,7 @@ def test_consecutive_chunks_grow_the_workspace(kind):
                 ring, S = ref[0]
                 exp = O.lin_chunk(ring, S, t, states, ws[0], LG.k_heads, LG.v_heads, LG.kd, LG.vd)
             mx, rr = _err(got, exp)
-            _say(f"chunk kind {kind} t0 {t} B {B}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"chunk kind {kind} t0 {t} B {B}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
             t += B
     finally:
@@ -338,7 +340,7 @@ def test_four_layer_stack_one_chunk():
                 ring, S = ref[L]
                 st_o = O.lin_chunk(ring, S, t0, st_o, ws[L], LG.k_heads, LG.v_heads, LG.kd, LG.vd)
             mx, rr = _err(st_g, st_o)
-            _say(f"stack chunk layer {L} kind {kind}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"stack chunk layer {L} kind {kind}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
     finally:
         ga.close()
@@ -372,7 +374,7 @@ def test_engine_order_chunks_then_decode():
                     st_o = O.lin_chunk(ring, S, t, st_o, ws[L], LG.k_heads, LG.v_heads, LG.kd,
                                        LG.vd)
             mx, rr = _err(st_g, st_o)
-            _say(f"engine order: chunk {n} (t0 {t}, B {B}) through 4 layers: max scaled err "
+            _say(f"engine order: chunk {n} (t0 {t}, B {B}) through 4 layers: max abs err "
                  f"{mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
             t += B
@@ -384,7 +386,7 @@ def test_engine_order_chunks_then_decode():
                 if kind == 2:
                     ref[L][t] = SY.bf16_round(ref[L][t])
             mx, rr = _err(st_g, st_o)
-            _say(f"engine order: decode token {t}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"engine order: decode token {t}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
             t += 1
         assert t == n_tok
@@ -475,7 +477,7 @@ def test_chunk_fp16_range_falls_back(kind):
     assert np.isfinite(got).all()
     mx, rr = _err(got, exp)
     _say(f"chunk kind {kind} with an fp16-range plant: status {bits}, |exp| max "
-         f"{np.abs(exp).max():.3e}, against the oracle: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+         f"{np.abs(exp).max():.3e}, against the oracle: max abs err {mx:.3e} rel-rms {rr:.3e}")
     assert bits & 2 and bits_after == bits
     assert np.array_equal(got, steps)
     assert rr <= ATOL
@@ -537,7 +539,7 @@ def test_layer_steps_from_trunk(tmp_path):
             for Lr, k in enumerate(kinds):
                 st_o = _oracle_layer(k, ref[Lr], ws[Lr], n_past + s, st_o)
             mx, rr = _err(got[s], st_o)
-            _say(f"trunk-loaded stack token {n_past + s}: max scaled err {mx:.3e} rel-rms {rr:.3e}")
+            _say(f"trunk-loaded stack token {n_past + s}: max abs err {mx:.3e} rel-rms {rr:.3e}")
             assert mx <= ATOL
             assert np.array_equal(got[s], direct[s])
         # a layer without its k_norm: incomplete, so a silent skip (state
