@@ -91,6 +91,63 @@ def test_gqa_prefill_4096_every_token():
     ga.close()
 
 
+@pytest.mark.parametrize("t0,B", [(32704, 64), (32749, 37)])
+def test_gqa_prefill_chunk_on_long_cache(t0, B):
+    """A prefill chunk on top of a long cache, as the engine's chunked prompt
+    reaches it at 32K context (aligned and unaligned t0).  The device draws
+    the t0 prefix rows into its bf16 cache (ds4f_hip_synth_gqa_cache) and the
+    chunk attends to all of them and causally to its own rows.  Every token
+    is checked against the oracle's body over the same prefix rows and the
+    oracle's own rows for the chunk, on a thread pool as in the 4096-token
+    test; the prefix rows stay untouched and the chunk's rows are the
+    oracle's in bf16."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from ds4f_hip.lib import check, load
+
+    _say(f"gqa prefill chunk t0={t0} B={B} over a drawn cache")
+    max_tokens = t0 + B + 8
+    cache = KvCache(1, max_tokens)
+    ga = GpuAttention([2], max_tokens, cache)
+    try:
+        check(load().ds4f_hip_synth_gqa_cache(0, t0, 0, S.tid(S.GQA_KCACHE, 0),
+                                              S.tid(S.GQA_VCACHE, 0), None), "synth kv")
+        ga.sync(0, to_host=True, n_kv_tokens=t0)
+        kv = cache.kv[0].copy()
+        assert np.abs(kv[:t0]).max() > 0
+        qn, kn = W.gqa_weights(GQ)
+        q, k, v = W.gqa_prefill_tokens(GQ, B)
+        out, kp = ga.gqa_prefill(0, t0, q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1), qn, kn)
+        kv[t0:t0 + B] = O.gqa_cache_rows(k, v, kn, t0, GQ.kv_heads, GQ.head_dim)
+        half = GQ.kv_heads * GQ.head_dim
+        assert np.abs(kp - kv[t0:t0 + B, :half]).max() < 1e-5
+
+        def worst_of(part):
+            kvc = kv.copy()      # the body rewrites row t0 + b with the helper's values
+            w = 0.0
+            for b in part:
+                o, _ = O.gqa_body(kvc, t0 + b, q[b].reshape(-1), k[b].reshape(-1), v[b].reshape(-1),
+                                  qn, kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+                w = max(w, _err(out[b], o)[0])
+            return w
+
+        nthr = 16
+        parts = [list(range(i, B, nthr)) for i in range(nthr)]
+        with ThreadPoolExecutor(max_workers=nthr) as pool:
+            worst = max(pool.map(worst_of, parts))
+        _say(f"  all {B} tokens: worst max abs {worst:.3e}")
+        assert worst <= ATOL
+
+        prefix = kv[:t0].copy()
+        ga.sync(0, to_host=True, n_kv_tokens=t0 + B)
+        assert np.array_equal(cache.kv[0, :t0], prefix)
+        ref = kv[t0:t0 + B]
+        dev = cache.kv[0, t0:t0 + B]
+        assert (np.abs(dev - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-5).all()   # bf16 of the rows
+    finally:
+        ga.close()
+
+
 def test_gqa_prefill_continues_a_cache():
     """Chunked prefill: 100 tokens, then 77 more at t0 = 100 (unaligned),
     then one decode step; all against the oracle's serial body."""
