@@ -268,6 +268,55 @@ def test_gqa_chunk_4096_sampled():
         ga.close()
 
 
+def test_lin_chunk_4096_every_token():
+    """A 4096-token prefill chunk through a delta-rule layer (the prefill
+    workload's size; src/attn_qwen.c ds4f_attn_linear_chunk :977-1135), every
+    token's hidden state and the final recurrent state checked.  The oracle's
+    chunk runs its layer steps one token at a time with scalar 4-bit
+    matvecs (about a minute for 4096 tokens on one core), so the reference
+    here splits the same computation: the input norm and the four input
+    projections in float64 over all tokens, the oracle's serial body
+    (orc_lin_prefill: conv, norms, gates, delta rule, gated norm) over the
+    4096 tokens, and the output projection plus residual in float64.  That
+    split is pinned against the oracle's own chunk on the first 64 tokens
+    before it is used."""
+    T, PIN = 4096, 64
+    ga, ref, ws = _stack([1], 0, 0, T + 64)
+    try:
+        _say(f"delta-rule chunk T={T}")
+        w, c = ws[0], ws[0].core
+        states = np.stack([W.hidden_state(HID, 0, 5000 + b) for b in range(T)])
+        got = ga.attn_chunk(0, 0, states)
+        assert np.isfinite(got).all()
+        ring0, S0 = ref[0]
+        xin = F.rmsnorm(states, F.bf(w.in_norm))
+
+        def proj(m):
+            return (xin @ F.mlx4_dense(m).T).astype(np.float32)
+
+        qkv, z, a, b = proj(w.qkv), proj(w.z), proj(w.a), proj(w.b)
+        ring, S = ring0.copy(), S0.copy()
+        ro = O.lin_prefill(ring, S, 0, qkv, z, a, b, c.conv_w, c.A_log, c.dt_bias, c.norm_w,
+                           LG.k_heads, LG.v_heads, LG.kd, LG.vd)
+        ro = ro[0] if isinstance(ro, tuple) else ro
+        exp = states.astype(np.float64) + ro.astype(np.float64) @ F.mlx4_dense(w.out).T
+        pin = O.lin_chunk(ring0.copy(), S0.copy(), 0, states[:PIN], w, LG.k_heads, LG.v_heads,
+                          LG.kd, LG.vd)
+        d_pin = float(np.abs(exp[:PIN] - pin).max())
+        _say(f"  split reference against the oracle's chunk, {PIN} tokens: max |d| {d_pin:.3e}")
+        assert d_pin <= 1e-4
+        mx, rr = _err(got, exp)
+        worst_t = int(np.abs(got - exp).max(axis=1).argmax())
+        _say(f"  all {T} tokens: max abs err {mx:.3e} (token {worst_t}) rel-rms {rr:.3e}")
+        assert mx <= ATOL
+        ga.sync(0, to_host=True)
+        srel = float(np.abs(ga.cache.lin[0] - S).max() / np.abs(S).max())
+        _say(f"  state after the chunk: max rel {srel:.3e}")
+        assert srel <= 1e-4
+    finally:
+        ga.close()
+
+
 @pytest.mark.parametrize("kind", [2, 1])
 def test_chunk_past_the_cache_end(kind):
     """A chunk running past max_tokens updates the rows of the tokens that
