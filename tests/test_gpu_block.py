@@ -218,6 +218,83 @@ def test_chunk_matches_oracle(kind, t0, B):
         ga.close()
 
 
+def _chunk_passes(T, n_pass, graph):
+    """n_pass passes of a delta-rule layer's and a GQA layer's chunk of T
+    tokens from position 0 (the hidden states restored to the same input at
+    the start of every pass) through ds4f_hip_attn_chunk_async on a fresh
+    binding: all eager, or the first eager (it sizes the workspaces) and the
+    rest replays of one captured pass with eager device work between the
+    replays.  Returns the hidden states after every pass and the delta-rule
+    state and ring at the end."""
+    import ctypes
+
+    import torch
+
+    from ds4f_hip.attn import dptr
+
+    ga, ref, ws = _stack([1, 2], 0, 0, T + 64)
+    try:
+        dev = torch.device("cuda:0")
+        states0 = torch.tensor(np.stack([W.hidden_state(HID, 0, 1200 + b) for b in range(T)]),
+                               device=dev)
+        states = states0.clone()
+
+        def launch():
+            stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            states.copy_(states0)
+            for Lr in range(2):
+                rc = ga.lib.ds4f_hip_attn_chunk_async(Lr, 0, T, dptr(states), stream)
+                assert rc == 0, ga.lib.ds4f_gpu_last_error()
+
+        outs = []
+        launch()
+        torch.cuda.synchronize()
+        outs.append(states.cpu().numpy().copy())
+        if graph:
+            side = torch.cuda.Stream()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                launch()
+            torch.cuda.synchronize()
+        for _ in range(1, n_pass):
+            if graph:
+                g.replay()
+            else:
+                launch()
+            torch.cuda.synchronize()
+            outs.append(states.cpu().numpy().copy())
+            x = torch.randn(1 << 20, device=dev)             # eager work between passes
+            assert np.isfinite(float((x * x).sum()))
+            torch.cuda.synchronize()
+        ga.sync(-1, to_host=True, n_kv_tokens=T)
+        return outs, ga.cache.lin[0].copy(), ga.cache.conv[0].copy(), ga.cache.kv[1, :T].copy()
+    finally:
+        ga.close()
+
+
+def test_chunk_graph_replays_equal_eager_passes():
+    """The way the 40-layer prefill benchmark runs its chunks: captured once
+    and replayed.  Four passes of a delta-rule and a GQA layer's 200-token
+    chunk (four 64-token delta-rule chunks, the last one ragged; seven
+    32-key tiles), eager on one binding and as one eager pass plus three
+    replays on a fresh binding of the same state: every pass's hidden states
+    bit for bit equal, and so the delta-rule state and ring, which advance
+    with every pass, and the GQA cache rows the passes write.  A memset or
+    a library reduction recorded into the graph would show here as a
+    replay that differs from its eager pass."""
+    T, n = 200, 4
+    _say(f"chunk graph: {n} passes of T={T}, eager against one eager pass + replays")
+    e_out, e_S, e_ring, e_kv = _chunk_passes(T, n, graph=False)
+    g_out, g_S, g_ring, g_kv = _chunk_passes(T, n, graph=True)
+    for p in range(n):
+        d = int((e_out[p].view(np.uint32) != g_out[p].view(np.uint32)).sum())
+        _say(f"  pass {p}: {d} of {e_out[p].size} hidden values differ")
+        assert d == 0
+    assert not np.array_equal(e_out[0], e_out[1])        # the delta-rule state carried over
+    assert np.array_equal(e_S, g_S) and np.array_equal(e_ring, g_ring)
+    assert np.array_equal(e_kv, g_kv)
+
+
 def test_gqa_chunk_4096_sampled():
     """A 4096-token prefill chunk through a GQA layer from an empty cache
     (the prefill workload's size), its rows at about 150 sampled tokens (the
