@@ -172,8 +172,11 @@ def test_lin_decode_4096_steps_state():
 
 
 # ------------------------------------------------------------------ GQA
-@pytest.mark.parametrize("n_past", [4096, 0, 1, 15, 16, 17, 63, 64, 65, 1000, 8191, 32768,
-                                    131072, 262143])
+# 8193: 65 split-K chunks of 128 positions, the last holding one;
+# 16383 / 16384 / 16385: the split goes from 128 chunks of 128 positions to
+# 86 chunks of 192, the last one ragged (65)
+@pytest.mark.parametrize("n_past", [4096, 0, 1, 15, 16, 17, 63, 64, 65, 1000, 8191, 8193, 16383,
+                                    16384, 16385, 32768, 131072, 262143])
 def test_gqa_decode_step(n_past):
     max_tokens = max(n_past + 8, 64)
     _say(f"gqa decode n_past={n_past}")
