@@ -148,6 +148,55 @@ def test_gqa_prefill_chunk_on_long_cache(t0, B):
         ga.close()
 
 
+def test_gqa_prefill_second_4096_chunk():
+    """The second 4096-token chunk of an 8192-token prompt (t0 = 4096 over
+    4096 cached rows): every workgroup's pair of q blocks then also covers
+    the 128 prefix key tiles of 32.  About 190 tokens are checked against the
+    oracle's body over the prefix rows and the oracle's own rows for the
+    chunk: the block edges, the last token of every 32-key tile and random
+    ones, on a thread pool as in the 4096-token test."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    t0, B = 4096, 4096
+    _say(f"gqa prefill chunk t0={t0} B={B}")
+    kc, vc = W.gqa_cache(GQ, t0, 2, 0)
+    half = GQ.kv_heads * GQ.head_dim
+    cache = KvCache(1, t0 + B + 64)
+    cache.kv[0, :t0, :half] = kc.reshape(t0, half)
+    cache.kv[0, :t0, half:] = vc.reshape(t0, half)
+    kv = cache.kv[0].copy()
+    ga = GpuAttention([2], t0 + B + 64, cache, n_kv_tokens=t0)
+    try:
+        qn, kn = W.gqa_weights(GQ)
+        q, k, v = W.gqa_prefill_tokens(GQ, B)
+        out, kp = ga.gqa_prefill(0, t0, q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1), qn, kn)
+        assert np.isfinite(out).all()
+        kv[t0:t0 + B] = O.gqa_cache_rows(k, v, kn, t0, GQ.kv_heads, GQ.head_dim)
+        assert np.abs(kp - kv[t0:t0 + B, :half]).max() < 1e-5
+        rng = np.random.default_rng(5)
+        samples = sorted(set([0, 1, 15, 16, 17, 31, 32, 63, 64, 2047, 2048, 4095] +
+                             list(range(31, B, 32)) +
+                             [int(x) for x in rng.integers(0, B, 48)]))
+
+        def worst_of(part):
+            kvc = kv.copy()      # the body rewrites row t0 + b with the helper's values
+            w = 0.0
+            for b in part:
+                o, _ = O.gqa_body(kvc, t0 + b, q[b].reshape(-1), k[b].reshape(-1), v[b].reshape(-1),
+                                  qn, kn, GQ.heads, GQ.kv_heads, GQ.head_dim)
+                w = max(w, _err(out[b], o)[0])
+            return w
+
+        nthr = 16
+        parts = [samples[i::nthr] for i in range(nthr)]
+        with ThreadPoolExecutor(max_workers=nthr) as pool:
+            worst = max(pool.map(worst_of, parts))
+        _say(f"  {len(samples)} sampled tokens: worst max abs {worst:.3e}")
+        assert worst <= ATOL
+    finally:
+        ga.close()
+
+
 def test_gqa_prefill_continues_a_cache():
     """Chunked prefill: 100 tokens, then 77 more at t0 = 100 (unaligned),
     then one decode step; all against the oracle's serial body."""
