@@ -78,11 +78,16 @@ __device__ __forceinline__ int wslot(int r, int h) { return h ^ (((r >> 2) ^ (r 
 
 /* x rows -> (optional RMSNorm) -> fp16 hi / lo in word order, tiled, and
  * the group sums of hi + lo.  One workgroup per token row (rows >= M: zeros);
- * thread t takes words t, t + 256, ... of the row.  The norm is an fp32
+ * thread t takes words t, t + 256, ... of the row, XW of them: the
+ * instance is picked by K (1 at 2048, the input projections; 2 at 4096, the
+ * GQA output projection; 4 up to 8192), so no thread issues loads past the
+ * row (at K = 2048 an instance for 8192 issued nine dead loads a thread:
+ * range-checked, they read no memory, but each is still issued and waited
+ * for).  The norm is an fp32
  * square sum times the hardware rsq (about 1 ulp from the reference's double
  * sum and division, src/attn_qwen.c:142-157, far below the hi / lo split's
  * 22 bits). */
-constexpr int XW = 8192 / (8 * NT);     /* words a thread holds (K <= 8192) */
+template <int XW>
 __global__ __launch_bounds__(NT) void xprep_kernel(Q35Mlx4Xprep p) {
     const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const int nw = p.K / 8;
@@ -436,7 +441,13 @@ extern "C" hipError_t q35_mlx4_wt(const uint32_t *vals, uint32_t *wt, int N, int
 extern "C" hipError_t q35_mlx4_xprep(const Q35Mlx4Xprep *p, hipStream_t stream) {
     if (p->K % 64 != 0 || p->K > 8192 || p->Mpad % MT != 0 || p->M > p->Mpad || p->M < 1)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(xprep_kernel, dim3(p->Mpad), dim3(NT), 0, stream, *p);
+    const int words = p->K / 8;           /* words of a row, NT a thread-step */
+    if (words <= NT)
+        hipLaunchKernelGGL(xprep_kernel<1>, dim3(p->Mpad), dim3(NT), 0, stream, *p);
+    else if (words <= 2 * NT)
+        hipLaunchKernelGGL(xprep_kernel<2>, dim3(p->Mpad), dim3(NT), 0, stream, *p);
+    else
+        hipLaunchKernelGGL(xprep_kernel<4>, dim3(p->Mpad), dim3(NT), 0, stream, *p);
     return hipGetLastError();
 }
 
